@@ -1,0 +1,147 @@
+/*
+ * pqa.h -- C ABI of the MI355X (gfx950) attention backend for the
+ * rain1201/picolm_qwen C++ forward pass.
+ *
+ * The reference has no plugin or FFI API for this path: the attention is
+ * inline code in Model::forward (cpp/model.hpp:326-418) and
+ * Model::forward_batch (cpp/model.hpp:507-593). This header defines the
+ * boundary as that block's live-ins and live-outs: q/k/v of the layer,
+ * the position, the QK-norm weights, the RoPE rows and the KV cache in,
+ * the attention output xb out.
+ *
+ * Memory: the context owns the KV cache in HBM in the reference's layout
+ *   key_cache/val_cache: uint16 fp16 [n_layers][max_seq_len][n_kv_heads][head_dim]
+ * (cpp/model.hpp:160, allocated :1003-1006, indexed :355-356,:369-370,:388-389),
+ * the RoPE tables, the QK-norm weights, a workspace and one HIP stream.
+ * Every call is asynchronous on that stream unless its name ends in _host.
+ *
+ * Errors: every int function returns PQA_OK (0) or a negative PQA_ERR_*;
+ * pqa_last_error() gives the message. Nothing throws across the ABI.
+ * Threading: a context is used by one host thread at a time.
+ */
+#ifndef PQA_H
+#define PQA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PQA_OK 0
+#define PQA_ERR_ARG (-1)         /* bad pointer, shape or layer index */
+#define PQA_ERR_RANGE (-2)       /* position outside [0, max_seq_len) */
+#define PQA_ERR_UNSUPPORTED (-3) /* head_dim not in {64, 128} */
+#define PQA_ERR_HIP (-4)         /* a HIP runtime call failed */
+#define PQA_ERR_NOMEM (-5)       /* device allocation failed */
+
+typedef struct pqa_ctx pqa_ctx;
+
+/* RopeFn choices (cpp/model.hpp:176, picked by cpp/picolm.cpp:179-186). */
+typedef enum {
+    PQA_ROPE_NEOX_HALF = 0,         /* TensorOps::rope_qwen, cpp/tensor.hpp:201-283: pairs (i, i+hd/2) */
+    PQA_ROPE_LLAMA_X86_BLOCK8 = 1,  /* TensorOps::rope_llama on x86 (SSE2 path), cpp/tensor.hpp:290-346:
+                                       pairs (8b+j, 8b+4+j) at angle 4b+j -- what the reference runs */
+    PQA_ROPE_LLAMA_INTERLEAVED = 2  /* rope_llama scalar branch, cpp/tensor.hpp:347-368: pairs (2i, 2i+1) */
+} pqa_rope_t;
+
+/*
+ * Allocates the cache and uploads the RoPE tables. Replaces
+ * Model::allocate_run_state's KV/RoPE part (cpp/model.hpp:1003-1017).
+ * rope_cos/rope_sin: host, [max_seq_len][head_dim/2] (state.rope_cos/sin).
+ * head_dim must be 64 or 128 and n_heads a multiple of n_kv_heads
+ * (kv_mul, cpp/model.hpp:295). The cache starts zeroed, as the reference's
+ * std::vector does.
+ */
+int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_heads, int n_kv_heads,
+               int head_dim, int rope_style, const float* rope_cos, const float* rope_sin);
+
+/* QK-RMSNorm weights of one layer (state.attn_q_norm_w/attn_k_norm_w,
+ * cpp/model.hpp:170, :984-1001). Host [head_dim] each; NULL for both turns the
+ * norm off for that layer, as when the GGUF lacks attn_q_norm (:327-328). */
+int pqa_set_qk_norm(pqa_ctx* ctx, int layer, const float* q_norm_w, const float* k_norm_w);
+
+/*
+ * One decode step of one layer: the block of cpp/model.hpp:326-418.
+ * Q/K RMSNorm (if set), RoPE at pos, K and V rounded to fp16 (the reference's
+ * ties-away-from-zero rounding, cpp/quant.hpp:102-135) and written at row pos,
+ * then attention of every query head over rows 0..pos.
+ * q [n_heads*head_dim], k/v [n_kv_heads*head_dim], out [n_heads*head_dim]:
+ * fp32 DEVICE pointers. q/k/v are not modified (the reference normalises
+ * in place; the caller never reads them afterwards).
+ */
+int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
+               float* out);
+
+/*
+ * Prompt of n_tok tokens at positions start_pos..start_pos+n_tok-1: the token
+ * loop of cpp/model.hpp:493-593 for one layer. Token-major fp32 DEVICE
+ * pointers q [n_tok][n_heads*hd], k/v [n_tok][n_kv*hd], out [n_tok][n_heads*hd].
+ * Rows are appended first and attention is causal (token i reads rows
+ * 0..start_pos+i), which is what the reference's serial loop computes.
+ */
+int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q, const float* k,
+                const float* v, float* out);
+
+/* Host-pointer forms of the two calls above for a forward loop whose q/k/v
+ * live in host std::vectors (cpp/model.hpp state.q / xb2): copy in, run,
+ * copy out, synchronise. */
+int pqa_decode_host(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
+                    const float* v, float* out);
+int pqa_prefill_host(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q,
+                     const float* k, const float* v, float* out);
+
+/* Copy cache rows [pos0, pos0+n) of one layer between host and HBM, in the
+ * reference row layout (kv_dim uint16 per row). Synchronous. Either row
+ * pointer may be NULL to skip that half. */
+int pqa_kv_upload(pqa_ctx* ctx, int layer, int pos0, int n, const uint16_t* k_rows,
+                  const uint16_t* v_rows);
+int pqa_kv_download(pqa_ctx* ctx, int layer, int pos0, int n, uint16_t* k_rows, uint16_t* v_rows);
+
+/* Device base pointers of the whole cache ([n_layers][max_seq_len][kv_dim]). */
+int pqa_kv_cache(pqa_ctx* ctx, uint16_t** key_cache, uint16_t** val_cache);
+
+/* The context's HIP stream (a hipStream_t), for event timing or ordering. */
+void* pqa_stream(pqa_ctx* ctx);
+int pqa_sync(pqa_ctx* ctx);
+
+/* Message of the last failed call on ctx; ctx == NULL gives the calling
+ * thread's last pqa_create failure. */
+const char* pqa_last_error(const pqa_ctx* ctx);
+void pqa_destroy(pqa_ctx* ctx);
+
+/* RoPE table exactly as the reference builds it (cpp/model.hpp:1008-1017):
+ * theta = (float)pos / powf(base, (float)(2i)/(float)hd), cosf, sinf, on the
+ * host. cos_tab/sin_tab: [max_seq_len][head_dim/2]. */
+void pqa_rope_table(float rope_base, int head_dim, int max_seq_len, float* cos_tab, float* sin_tab);
+
+/* fp32 -> fp16 with the reference's rounding (cpp/quant.hpp:102-135) as a
+ * device op on n elements, on the context stream. DEVICE pointers. */
+int pqa_fp32_to_fp16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
+
+/*
+ * Benchmark and test helper with no counterpart in the reference: fills cache
+ * rows [pos0, pos0+n) of `layer` with seeded synthetic history on the device.
+ * K and V ~N(0,1) from SplitMix64 + Box-Muller (the same generator as the
+ * CPU oracle's pqo_synth_kv_rows), rows with uniform < outlier_prob scaled by
+ * 8, then fp16 by the reference rounding.
+ */
+int pqa_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float outlier_prob);
+
+/* Decode split size in cache rows per workgroup (a multiple of 64; 0 = the
+ * automatic choice). For tuning sweeps; results do not depend on it beyond
+ * fp32 summation order. */
+int pqa_set_decode_split(pqa_ctx* ctx, int rows_per_split);
+
+/* Prefill score precision. 0 (default): q is rounded once to fp16 for the
+ * QK^T MFMA, an error of about 2.5e-4 per score at unit-variance inputs.
+ * 1: q is carried as fp16 hi + lo (two MFMAs per step), fp32-level scores,
+ * for caches whose keys hold large outliers; costs 1.5x the MFMA work. */
+int pqa_set_prefill_precision(pqa_ctx* ctx, int split_q);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PQA_H */

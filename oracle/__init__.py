@@ -1,0 +1,328 @@
+"""ctypes bindings for the CPU oracle (liboracle.so) and the reference harness
+(_ref/libref_{A,B}.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline,
+never as a compute path of the product.
+
+Functions restated from the reference (rain1201/picolm_qwen) and the pin of
+each one (closed form, exhaustive KAT or golden vector) are listed in
+oracle/pqa_oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = {"A": os.path.join(HERE, "_ref", "libref_A.so"), "B": os.path.join(HERE, "_ref", "libref_B.so")}
+
+ROPE_NEOX_HALF, ROPE_LLAMA_X86_BLOCK8, ROPE_LLAMA_INTERLEAVED = 0, 1, 2
+KIND_Q, KIND_K, KIND_V, KIND_KHIST, KIND_VHIST, KIND_QNORM, KIND_KNORM, KIND_OUTLIER = range(1, 9)
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+
+
+class Shape(C.Structure):
+    _fields_ = [("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int),
+                ("max_seq_len", C.c_int), ("rope_style", C.c_int)]
+
+
+_lib = None
+
+
+def lib():
+    """Loads liboracle.so (built by `make -C oracle`)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(ORACLE_SO):
+        raise RuntimeError(f"oracle not built: {ORACLE_SO} missing (run make -C oracle)")
+    L = C.CDLL(ORACLE_SO)
+    L.pqo_fp16_to_fp32.restype = C.c_float
+    L.pqo_fp16_to_fp32.argtypes = [C.c_uint16]
+    L.pqo_fp32_to_fp16.restype = C.c_uint16
+    L.pqo_fp32_to_fp16.argtypes = [C.c_float]
+    L.pqo_fp16_to_fp32_array.argtypes = [_u16p, _f32p, C.c_size_t]
+    L.pqo_fp32_to_fp16_array.argtypes = [_f32p, _u16p, C.c_size_t]
+    L.pqo_fp32_bits_to_fp16_range.argtypes = [C.c_uint32, C.c_size_t, _u16p, C.c_int]
+    L.pqo_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int]
+    L.pqo_rope.argtypes = [C.c_int, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+    L.pqo_rope_table.argtypes = [C.c_float, C.c_int, C.c_int, _f32p, _f32p]
+    L.pqo_rope_rows.argtypes = [C.c_float, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+    vp = C.c_void_p
+    L.pqo_attn_step.argtypes = [C.POINTER(Shape), C.c_int, _f32p, _f32p, _f32p, vp, vp, _f32p, _f32p,
+                                _u16p, _u16p, _f32p, C.c_int]
+    L.pqo_attend.argtypes = [C.POINTER(Shape), C.c_int, _f32p, _u16p, _u16p, _f32p, C.c_int]
+    L.pqo_append.argtypes = [C.POINTER(Shape), C.c_int, _f32p, _f32p, _f32p, vp, vp, _f32p, _f32p,
+                             _u16p, _u16p]
+    L.pqo_prefill.argtypes = [C.POINTER(Shape), C.c_int, C.c_int, _f32p, _f32p, _f32p, vp, vp, _f32p,
+                              _f32p, _u16p, _u16p, _f32p, C.c_int, C.c_int]
+    L.pqo_attend_f64.argtypes = [C.POINTER(Shape), C.c_int, _f32p, _u16p, _u16p, _f64p]
+    L.pqo_splitmix64.restype = C.c_uint64
+    L.pqo_splitmix64.argtypes = [C.c_uint64, C.c_uint64]
+    L.pqo_stream_key.restype = C.c_uint64
+    L.pqo_stream_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32]
+    L.pqo_normal.restype = C.c_float
+    L.pqo_normal.argtypes = [C.c_uint64, C.c_uint64]
+    L.pqo_fill_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, _f32p]
+    L.pqo_is_outlier.restype = C.c_int
+    L.pqo_is_outlier.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64, C.c_float]
+    L.pqo_synth_kv_rows.argtypes = [C.c_uint64, C.c_uint32, C.c_int, C.c_int, C.c_int, C.c_float,
+                                    _u16p, _u16p, C.c_int]
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def shape(n_heads, n_kv_heads, head_dim, max_seq_len, rope_style):
+    return Shape(n_heads, n_kv_heads, head_dim, max_seq_len, rope_style)
+
+
+# ---- numerics -------------------------------------------------------------
+
+def fp32_to_fp16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().pqo_fp32_to_fp16_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def fp16_to_fp32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().pqo_fp16_to_fp32_array(h.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def fp32_bits_to_fp16(first, n, n_threads=8):
+    out = np.empty(n, dtype=np.uint16)
+    lib().pqo_fp32_bits_to_fp16_range(first, n, out, n_threads)
+    return out
+
+
+def rmsnorm(x, w):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().pqo_rmsnorm(out, x, np.ascontiguousarray(w, dtype=np.float32), x.size)
+    return out
+
+
+def rope(style, q, k, head_dim, n_heads, n_kv_heads, cos_row, sin_row):
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    lib().pqo_rope(style, q.reshape(-1), k.reshape(-1), head_dim, n_heads, n_kv_heads,
+                   np.ascontiguousarray(cos_row, dtype=np.float32),
+                   np.ascontiguousarray(sin_row, dtype=np.float32))
+    return q, k
+
+
+def rope_table(base, head_dim, max_seq_len):
+    half = head_dim // 2
+    c = np.empty((max_seq_len, half), dtype=np.float32)
+    s = np.empty((max_seq_len, half), dtype=np.float32)
+    lib().pqo_rope_table(base, head_dim, max_seq_len, c.reshape(-1), s.reshape(-1))
+    return c, s
+
+
+def rope_rows(base, head_dim, pos0, n):
+    half = head_dim // 2
+    c = np.empty((n, half), dtype=np.float32)
+    s = np.empty((n, half), dtype=np.float32)
+    lib().pqo_rope_rows(base, head_dim, pos0, n, c.reshape(-1), s.reshape(-1))
+    return c, s
+
+
+def attn_step(shp, pos, q, k, v, q_norm_w, k_norm_w, cos_row, sin_row, kc, vc, n_threads=1):
+    """Decode block at `pos`; kc/vc (layer slice, uint16 [S_max, kv_dim]) are updated in place."""
+    out = np.empty(shp.n_heads * shp.head_dim, dtype=np.float32)
+    qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, dtype=np.float32)
+    kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, dtype=np.float32)
+    lib().pqo_attn_step(C.byref(shp), pos, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+                        np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
+                        np.ascontiguousarray(v, dtype=np.float32).reshape(-1), _ptr(qn), _ptr(kn),
+                        np.ascontiguousarray(cos_row, dtype=np.float32).reshape(-1),
+                        np.ascontiguousarray(sin_row, dtype=np.float32).reshape(-1),
+                        kc.reshape(-1), vc.reshape(-1), out, n_threads)
+    return out
+
+
+def attend(shp, pos, q, kc, vc, n_threads=1):
+    out = np.empty(shp.n_heads * shp.head_dim, dtype=np.float32)
+    lib().pqo_attend(C.byref(shp), pos, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+                     kc.reshape(-1), vc.reshape(-1), out, n_threads)
+    return out
+
+
+def append(shp, pos, q, k, v, q_norm_w, k_norm_w, cos_row, sin_row, kc, vc):
+    """Norm + RoPE + fp16 append; returns the normed, roped q."""
+    q = np.array(q, dtype=np.float32, copy=True).reshape(-1)
+    qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, dtype=np.float32)
+    kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, dtype=np.float32)
+    lib().pqo_append(C.byref(shp), pos, q, np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
+                     np.ascontiguousarray(v, dtype=np.float32).reshape(-1), _ptr(qn), _ptr(kn),
+                     np.ascontiguousarray(cos_row, dtype=np.float32).reshape(-1),
+                     np.ascontiguousarray(sin_row, dtype=np.float32).reshape(-1),
+                     kc.reshape(-1), vc.reshape(-1))
+    return q
+
+
+def prefill(shp, start, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, kc, vc, serial=False,
+            n_threads=8):
+    n_tok = q.shape[0]
+    out = np.empty((n_tok, shp.n_heads * shp.head_dim), dtype=np.float32)
+    qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, dtype=np.float32)
+    kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, dtype=np.float32)
+    lib().pqo_prefill(C.byref(shp), start, n_tok, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+                      np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
+                      np.ascontiguousarray(v, dtype=np.float32).reshape(-1), _ptr(qn), _ptr(kn),
+                      np.ascontiguousarray(cos_tab, dtype=np.float32).reshape(-1),
+                      np.ascontiguousarray(sin_tab, dtype=np.float32).reshape(-1),
+                      kc.reshape(-1), vc.reshape(-1), out.reshape(-1), 1 if serial else 0, n_threads)
+    return out
+
+
+def attend_f64(shp, pos, q, kc, vc):
+    out = np.empty(shp.n_heads * shp.head_dim, dtype=np.float64)
+    lib().pqo_attend_f64(C.byref(shp), pos, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+                         kc.reshape(-1), vc.reshape(-1), out)
+    return out
+
+
+# ---- synthetic inputs -------------------------------------------------------
+
+def stream_key(seed, kind, layer):
+    return lib().pqo_stream_key(seed, kind, layer)
+
+
+def normal(seed, kind, layer, first, n, mean=0.0, std=1.0):
+    out = np.empty(n, dtype=np.float32)
+    lib().pqo_fill_normal(stream_key(seed, kind, layer), first, n, mean, std, out)
+    return out
+
+
+def synth_kv_rows(seed, layer, kv_dim, pos0, n, outlier_prob=0.0, n_threads=8):
+    k = np.empty((n, kv_dim), dtype=np.uint16)
+    v = np.empty((n, kv_dim), dtype=np.uint16)
+    if n > 0:
+        lib().pqo_synth_kv_rows(seed, layer, kv_dim, pos0, n, outlier_prob, k.reshape(-1), v.reshape(-1),
+                                n_threads)
+    return k, v
+
+
+def step_inputs(seed, layer, token, n_heads, n_kv_heads, head_dim):
+    """q/k/v fp32 ~N(0,1) of one token (index `token` of the layer's streams)."""
+    q_dim, kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+    q = normal(seed, KIND_Q, layer, token * q_dim, q_dim)
+    k = normal(seed, KIND_K, layer, token * kv_dim, kv_dim)
+    v = normal(seed, KIND_V, layer, token * kv_dim, kv_dim)
+    return q, k, v
+
+
+def batch_inputs(seed, layer, start_token, n_tok, n_heads, n_kv_heads, head_dim):
+    q_dim, kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+    q = normal(seed, KIND_Q, layer, start_token * q_dim, n_tok * q_dim).reshape(n_tok, q_dim)
+    k = normal(seed, KIND_K, layer, start_token * kv_dim, n_tok * kv_dim).reshape(n_tok, kv_dim)
+    v = normal(seed, KIND_V, layer, start_token * kv_dim, n_tok * kv_dim).reshape(n_tok, kv_dim)
+    return q, k, v
+
+
+def qk_norm_weights(seed, layer, head_dim):
+    """QK-RMSNorm weights ~N(1, 0.02)."""
+    return (normal(seed, KIND_QNORM, layer, 0, head_dim, 1.0, 0.02),
+            normal(seed, KIND_KNORM, layer, 0, head_dim, 1.0, 0.02))
+
+
+# ---- reference harness (only where it was built) -----------------------------
+
+class RefModel:
+    """The reference's Model::forward driven through oracle/ref_harness.cpp."""
+
+    _libs = {}
+
+    @classmethod
+    def available(cls, variant="B"):
+        return os.path.exists(REF_SO[variant])
+
+    @classmethod
+    def load(cls, variant="B"):
+        if variant in cls._libs:
+            return cls._libs[variant]
+        L = C.CDLL(REF_SO[variant])
+        L.ref_open.restype = C.c_void_p
+        L.ref_open.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int]
+        L.ref_set_qk_norm.argtypes = [C.c_void_p, _f32p, _f32p]
+        L.ref_set_cache_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, _u16p, _u16p]
+        L.ref_get_cache_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, _u16p, _u16p]
+        L.ref_get_rope_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, _f32p, _f32p]
+        L.ref_step.argtypes = [C.c_void_p, C.c_int, _f32p, _f32p, _f32p, _f32p]
+        L.ref_close.argtypes = [C.c_void_p]
+        L.ref_fp32_bits_to_fp16_range.argtypes = [C.c_uint32, C.c_size_t, _u16p]
+        L.ref_fp16_to_fp32_all.argtypes = [_f32p]
+        L.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int]
+        L.ref_rope.argtypes = [C.c_int, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+        cls._libs[variant] = L
+        return L
+
+    def __init__(self, n_heads, n_kv_heads, head_dim, max_seq_len, rope_base, rope_qwen, qk_norm,
+                 variant="B", path=None):
+        import tempfile
+        self.L = self.load(variant)
+        self.nh, self.nkv, self.hd, self.smax = n_heads, n_kv_heads, head_dim, max_seq_len
+        fd, self.path = tempfile.mkstemp(suffix=".gguf") if path is None else (None, path)
+        if fd is not None:
+            os.close(fd)
+        self.h = self.L.ref_open(self.path.encode(), n_heads, n_kv_heads, head_dim, max_seq_len,
+                                 rope_base, int(rope_qwen), int(qk_norm))
+        if not self.h:
+            raise RuntimeError("reference Model::load failed")
+
+    def set_qk_norm(self, qw, kw):
+        self.L.ref_set_qk_norm(self.h, np.ascontiguousarray(qw, np.float32), np.ascontiguousarray(kw, np.float32))
+
+    def set_cache_rows(self, pos0, k, v):
+        n = k.shape[0]
+        if n:
+            self.L.ref_set_cache_rows(self.h, pos0, n, np.ascontiguousarray(k).reshape(-1),
+                                      np.ascontiguousarray(v).reshape(-1))
+
+    def cache_rows(self, pos0, n):
+        kv = self.nkv * self.hd
+        k = np.empty((n, kv), np.uint16)
+        v = np.empty((n, kv), np.uint16)
+        self.L.ref_get_cache_rows(self.h, pos0, n, k.reshape(-1), v.reshape(-1))
+        return k, v
+
+    def rope_rows(self, pos0, n):
+        half = self.hd // 2
+        c = np.empty((n, half), np.float32)
+        s = np.empty((n, half), np.float32)
+        self.L.ref_get_rope_rows(self.h, pos0, n, c.reshape(-1), s.reshape(-1))
+        return c, s
+
+    def step(self, pos, q, k, v):
+        out = np.empty(self.nh * self.hd, np.float32)
+        self.L.ref_step(self.h, pos, np.ascontiguousarray(q, np.float32), np.ascontiguousarray(k, np.float32),
+                        np.ascontiguousarray(v, np.float32), out)
+        return out
+
+    def close(self):
+        if self.h:
+            self.L.ref_close(self.h)
+            self.h = None
+        if self.path and os.path.exists(self.path):
+            os.unlink(self.path)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,60 @@
+"""Builds libpqa.so (the HIP backend behind include/pqa.h) in-tree with hipcc
+for gfx950."""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import tempfile
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libpqa.so")
+SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# -ffp-contract=off: the K row written to the cache must round like the
+# reference (no fused multiply-add in RMSNorm or RoPE); kernels that want an
+# FMA call fmaf() explicitly. Packed fp32 instructions are disabled.
+CFLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
+
+
+def _compile(src: str, obj: str) -> None:
+    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every csrc/*.hip source and links libpqa.so; returns its path."""
+    with tempfile.TemporaryDirectory(prefix="pqa_build_") as tmp:
+        objs = [os.path.join(tmp, s.replace(".hip", ".o")) for s in SOURCES]
+        with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+            list(ex.map(_compile, SOURCES, objs))
+        tmp_lib = LIB + ".tmp"
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp_lib, *objs]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+        os.replace(tmp_lib, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+def build_oracle(with_reference: bool = True) -> None:
+    """Builds the CPU oracle (test infrastructure) and, when the reference tree
+    is present, the reference harness into oracle/_ref/."""
+    odir = os.path.join(ROOT, "oracle")
+    subprocess.run(["make", "-s", "-C", odir, "-B", "liboracle.so"], check=True)
+    if with_reference and os.path.isdir("/root/reference/cpp"):
+        subprocess.run(["make", "-s", "-C", odir, "-B", "ref"], check=True)
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    build_oracle()

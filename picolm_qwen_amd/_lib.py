@@ -1,0 +1,75 @@
+"""ctypes binding of libpqa.so (include/pqa.h). Loading fails loudly: there is
+no CPU fallback for any entry point."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from ._build import LIB
+
+PQA_OK = 0
+PQA_ERR_ARG = -1
+PQA_ERR_RANGE = -2
+PQA_ERR_UNSUPPORTED = -3
+PQA_ERR_HIP = -4
+PQA_ERR_NOMEM = -5
+
+EXPORTS = [
+    "pqa_create", "pqa_set_qk_norm", "pqa_decode", "pqa_prefill", "pqa_decode_host",
+    "pqa_prefill_host", "pqa_kv_upload", "pqa_kv_download", "pqa_kv_cache", "pqa_stream",
+    "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
+    "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision",
+]
+
+
+class PQAError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"pqa error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB):
+        raise RuntimeError(f"{LIB} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+    L = C.CDLL(LIB)
+    vp, i, f, u64, sz = C.c_void_p, C.c_int, C.c_float, C.c_uint64, C.c_size_t
+    fp = C.POINTER(C.c_float)
+    L.pqa_create.argtypes = [C.POINTER(vp), i, i, i, i, i, i, vp, vp]
+    L.pqa_set_qk_norm.argtypes = [vp, i, vp, vp]
+    L.pqa_decode.argtypes = [vp, i, i, vp, vp, vp, vp]
+    L.pqa_prefill.argtypes = [vp, i, i, i, vp, vp, vp, vp]
+    L.pqa_decode_host.argtypes = [vp, i, i, vp, vp, vp, vp]
+    L.pqa_prefill_host.argtypes = [vp, i, i, i, vp, vp, vp, vp]
+    L.pqa_kv_upload.argtypes = [vp, i, i, i, vp, vp]
+    L.pqa_kv_download.argtypes = [vp, i, i, i, vp, vp]
+    L.pqa_kv_cache.argtypes = [vp, C.POINTER(vp), C.POINTER(vp)]
+    L.pqa_stream.argtypes = [vp]
+    L.pqa_stream.restype = vp
+    L.pqa_sync.argtypes = [vp]
+    L.pqa_last_error.argtypes = [vp]
+    L.pqa_last_error.restype = C.c_char_p
+    L.pqa_destroy.argtypes = [vp]
+    L.pqa_destroy.restype = None
+    L.pqa_rope_table.argtypes = [f, i, i, fp, fp]
+    L.pqa_rope_table.restype = None
+    L.pqa_fp32_to_fp16.argtypes = [vp, vp, vp, sz]
+    L.pqa_synth_kv.argtypes = [vp, i, i, i, u64, f]
+    L.pqa_set_decode_split.argtypes = [vp, i]
+    L.pqa_set_prefill_precision.argtypes = [vp, i]
+    for name in EXPORTS:
+        if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
+            getattr(L, name).restype = C.c_int
+    _lib = L
+    return L
+
+
+def check(rc: int, ctx=None) -> None:
+    if rc != PQA_OK:
+        msg = lib().pqa_last_error(ctx)
+        raise PQAError(rc, msg.decode() if msg else "")

@@ -1,0 +1,232 @@
+"""Host-side mirror of the reference's attention block over the HIP backend.
+
+The reference (rain1201/picolm_qwen) runs the block inline in
+Model::forward(token, pos) (cpp/model.hpp:288, block :326-418) and
+Model::forward_batch(tokens, start_pos) (cpp/model.hpp:462, block :507-593),
+with the KV cache and RoPE tables in its RunState (cpp/model.hpp:158-174).
+`PicoAttention` owns that state in HBM and exposes the block per layer with the
+same argument meaning:
+
+    forward(layer, pos, q, k, v)              decode at pos (append, attend 0..pos)
+    forward_batch(layer, start_pos, q, k, v)  prompt rows start_pos.. (token-major)
+
+q/k/v may be torch tensors on the GPU (device path, asynchronous on the
+context stream) or host numpy arrays (copy in, run, copy out). Every call
+goes through libpqa.so; a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import check, lib
+
+ROPE_NEOX_HALF = 0          # rope_qwen       cpp/tensor.hpp:201-283
+ROPE_LLAMA_X86_BLOCK8 = 1   # rope_llama SSE2 cpp/tensor.hpp:290-346 (x86 reference)
+ROPE_LLAMA_INTERLEAVED = 2  # rope_llama scalar cpp/tensor.hpp:347-368
+
+
+def rope_table(rope_base: float, head_dim: int, max_seq_len: int):
+    """RoPE table rows [max_seq_len][head_dim/2] as cpp/model.hpp:1008-1017 builds it."""
+    half = head_dim // 2
+    c = np.empty((max_seq_len, half), dtype=np.float32)
+    s = np.empty((max_seq_len, half), dtype=np.float32)
+    fp = C.POINTER(C.c_float)
+    lib().pqa_rope_table(rope_base, head_dim, max_seq_len, c.ctypes.data_as(fp), s.ctypes.data_as(fp))
+    return c, s
+
+
+def _is_torch(x) -> bool:
+    return type(x).__module__.startswith("torch")
+
+
+def _dev_ptr(t, dtype_name: str, numel: int):
+    if not t.is_cuda:
+        raise ValueError("torch tensors must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensors must be contiguous")
+    if str(t.dtype) != "torch." + dtype_name:
+        raise ValueError(f"expected {dtype_name}, got {t.dtype}")
+    if t.numel() != numel:
+        raise ValueError(f"expected {numel} elements, got {t.numel()}")
+    return C.c_void_p(t.data_ptr())
+
+
+def _host(x, numel: int):
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    if a.size != numel:
+        raise ValueError(f"expected {numel} elements, got {a.size}")
+    return a
+
+
+class PicoAttention:
+    def __init__(self, n_layers: int, max_seq_len: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                 rope_style: int = ROPE_NEOX_HALF, rope_base: float = 10000.0, rope_cos=None, rope_sin=None):
+        if rope_cos is None or rope_sin is None:
+            rope_cos, rope_sin = rope_table(rope_base, head_dim, max_seq_len)
+        rope_cos = np.ascontiguousarray(rope_cos, dtype=np.float32)
+        rope_sin = np.ascontiguousarray(rope_sin, dtype=np.float32)
+        if rope_cos.size != max_seq_len * (head_dim // 2) or rope_sin.size != rope_cos.size:
+            raise ValueError("RoPE tables must be [max_seq_len][head_dim/2]")
+        self.n_layers, self.max_seq_len = n_layers, max_seq_len
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        self.q_dim, self.kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+        self.rope_style = rope_style
+        h = C.c_void_p()
+        check(lib().pqa_create(C.byref(h), n_layers, max_seq_len, n_heads, n_kv_heads, head_dim, rope_style,
+                               rope_cos.ctypes.data_as(C.c_void_p), rope_sin.ctypes.data_as(C.c_void_p)))
+        self._h = h
+
+    # -- lifecycle ---------------------------------------------------------
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise RuntimeError("context destroyed")
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            self._ext = None
+            lib().pqa_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def stream(self) -> int:
+        """The context's hipStream_t as an int (torch.cuda.ExternalStream(stream))."""
+        return lib().pqa_stream(self.handle) or 0
+
+    def sync(self) -> None:
+        check(lib().pqa_sync(self.handle), self.handle)
+
+    def _ext_stream(self, device):
+        import torch
+        s = getattr(self, "_ext", None)
+        if s is None:
+            s = torch.cuda.ExternalStream(self.stream, device=device)
+            self._ext = s
+        return s
+
+    def _enter(self, device, tensors):
+        # The context stream waits for torch's current stream, so the inputs are
+        # ready. The tensors are NOT record_stream()ed on the context stream:
+        # torch would record events on it when they are freed, possibly after
+        # the context (and its stream) is destroyed. _leave() orders torch's
+        # stream after the call instead, which also covers the allocator
+        # reusing the blocks.
+        import torch
+        ext = self._ext_stream(device)
+        ext.wait_stream(torch.cuda.current_stream(device))
+        return ext
+
+    def _leave(self, device, ext):
+        import torch
+        torch.cuda.current_stream(device).wait_stream(ext)
+
+    def set_decode_split(self, rows_per_split: int) -> None:
+        check(lib().pqa_set_decode_split(self.handle, rows_per_split), self.handle)
+
+    def set_prefill_precision(self, split_q: bool) -> None:
+        """True: prefill scores from q as fp16 hi+lo (for keys with large outliers)."""
+        check(lib().pqa_set_prefill_precision(self.handle, int(bool(split_q))), self.handle)
+
+    # -- the block ----------------------------------------------------------
+    def set_qk_norm(self, layer: int, q_norm_w, k_norm_w) -> None:
+        """Layer's attn_q_norm / attn_k_norm weights ([head_dim] each); None turns it off."""
+        if q_norm_w is None and k_norm_w is None:
+            check(lib().pqa_set_qk_norm(self.handle, layer, None, None), self.handle)
+            return
+        qw = _host(q_norm_w, self.head_dim)
+        kw = _host(k_norm_w, self.head_dim)
+        check(lib().pqa_set_qk_norm(self.handle, layer, qw.ctypes.data_as(C.c_void_p),
+                                    kw.ctypes.data_as(C.c_void_p)), self.handle)
+
+    def forward(self, layer: int, pos: int, q, k, v, out=None):
+        """Decode block at `pos` (cpp/model.hpp:326-418); returns xb [n_heads*head_dim]."""
+        if _is_torch(q):
+            import torch
+            if out is None:
+                out = torch.empty(self.q_dim, dtype=torch.float32, device=q.device)
+            ext = self._enter(q.device, (q, k, v, out))
+            check(lib().pqa_decode(self.handle, layer, pos, _dev_ptr(q, "float32", self.q_dim),
+                                   _dev_ptr(k, "float32", self.kv_dim), _dev_ptr(v, "float32", self.kv_dim),
+                                   _dev_ptr(out, "float32", self.q_dim)), self.handle)
+            self._leave(q.device, ext)
+            return out
+        qh, kh, vh = _host(q, self.q_dim), _host(k, self.kv_dim), _host(v, self.kv_dim)
+        res = np.empty(self.q_dim, dtype=np.float32) if out is None else out
+        check(lib().pqa_decode_host(self.handle, layer, pos, qh.ctypes.data_as(C.c_void_p),
+                                    kh.ctypes.data_as(C.c_void_p), vh.ctypes.data_as(C.c_void_p),
+                                    res.ctypes.data_as(C.c_void_p)), self.handle)
+        return res
+
+    def forward_batch(self, layer: int, start_pos: int, q, k, v, out=None):
+        """Prompt rows start_pos..start_pos+n-1 (cpp/model.hpp:493-593); q [n][q_dim],
+        k/v [n][kv_dim]; returns out [n][q_dim]."""
+        n_tok = int(q.shape[0])
+        if _is_torch(q):
+            import torch
+            if out is None:
+                out = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=q.device)
+            ext = self._enter(q.device, (q, k, v, out))
+            check(lib().pqa_prefill(self.handle, layer, start_pos, n_tok,
+                                    _dev_ptr(q, "float32", n_tok * self.q_dim),
+                                    _dev_ptr(k, "float32", n_tok * self.kv_dim),
+                                    _dev_ptr(v, "float32", n_tok * self.kv_dim),
+                                    _dev_ptr(out, "float32", n_tok * self.q_dim)), self.handle)
+            self._leave(q.device, ext)
+            return out
+        qh = _host(q, n_tok * self.q_dim)
+        kh, vh = _host(k, n_tok * self.kv_dim), _host(v, n_tok * self.kv_dim)
+        res = np.empty((n_tok, self.q_dim), dtype=np.float32) if out is None else out
+        check(lib().pqa_prefill_host(self.handle, layer, start_pos, n_tok, qh.ctypes.data_as(C.c_void_p),
+                                     kh.ctypes.data_as(C.c_void_p), vh.ctypes.data_as(C.c_void_p),
+                                     res.ctypes.data_as(C.c_void_p)), self.handle)
+        return res
+
+    # -- cache access ---------------------------------------------------------
+    def kv_download(self, layer: int, pos0: int, n: int):
+        """Rows [pos0, pos0+n) as uint16 [n][kv_dim] (state.key_cache/val_cache bytes)."""
+        k = np.empty((n, self.kv_dim), dtype=np.uint16)
+        v = np.empty((n, self.kv_dim), dtype=np.uint16)
+        check(lib().pqa_kv_download(self.handle, layer, pos0, n, k.ctypes.data_as(C.c_void_p),
+                                    v.ctypes.data_as(C.c_void_p)), self.handle)
+        return k, v
+
+    def kv_upload(self, layer: int, pos0: int, k_rows, v_rows) -> None:
+        k = np.ascontiguousarray(k_rows, dtype=np.uint16)
+        v = np.ascontiguousarray(v_rows, dtype=np.uint16)
+        n = k.size // self.kv_dim
+        if k.size != n * self.kv_dim or v.size != k.size:
+            raise ValueError("rows must be [n][kv_dim] uint16")
+        check(lib().pqa_kv_upload(self.handle, layer, pos0, n, k.ctypes.data_as(C.c_void_p),
+                                  v.ctypes.data_as(C.c_void_p)), self.handle)
+
+    def kv_cache_ptrs(self):
+        kp, vp = C.c_void_p(), C.c_void_p()
+        check(lib().pqa_kv_cache(self.handle, C.byref(kp), C.byref(vp)), self.handle)
+        return kp.value, vp.value
+
+    def synth_kv(self, layer: int, pos0: int, n: int, seed: int, outlier_prob: float = 0.0) -> None:
+        """Seeded synthetic history rows (same generator as the CPU oracle)."""
+        check(lib().pqa_synth_kv(self.handle, layer, pos0, n, seed, outlier_prob), self.handle)
+
+    def fp32_to_fp16(self, src, dst) -> None:
+        """Device fp32 -> fp16 with the reference rounding (torch tensors on the GPU)."""
+        n = src.numel()
+        ext = self._enter(src.device, (src, dst))
+        check(lib().pqa_fp32_to_fp16(self.handle, _dev_ptr(src, "float32", n), _dev_ptr(dst, "int16", n), n),
+              self.handle)
+        self._leave(src.device, ext)

@@ -1,0 +1,313 @@
+// The extern "C" boundary (include/pqa.h): argument checks, HBM ownership,
+// host staging, error reporting. Kernels live in pqa_decode.hip,
+// pqa_prefill.hip and pqa_util.hip.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "pqa_internal.h"
+
+static thread_local std::string g_create_err;
+
+namespace pqa {
+
+int set_err(pqa_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    else g_create_err = msg;
+    return code;
+}
+
+int hip_check(pqa_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return PQA_OK;
+    const int code = e == hipErrorOutOfMemory ? PQA_ERR_NOMEM : PQA_ERR_HIP;
+    return set_err(ctx, code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace pqa
+
+using pqa::hip_check;
+using pqa::set_err;
+
+static void free_ctx(pqa_ctx* c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm,
+                    c->part_acc,  c->part_ml,   c->counters, c->q16,      c->stage};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+template <typename T>
+static hipError_t dev_alloc(T** p, size_t count) {
+    return hipMalloc((void**)p, std::max<size_t>(count, 1) * sizeof(T));
+}
+
+extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_heads, int n_kv_heads,
+                          int head_dim, int rope_style, const float* rope_cos, const float* rope_sin) {
+    if (!out) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: out is NULL");
+    *out = nullptr;
+    if (n_layers <= 0 || max_seq_len <= 0 || n_heads <= 0 || n_kv_heads <= 0)
+        return set_err(nullptr, PQA_ERR_ARG, "pqa_create: sizes must be positive");
+    if (n_heads % n_kv_heads != 0)
+        return set_err(nullptr, PQA_ERR_ARG, "pqa_create: n_heads must be a multiple of n_kv_heads");
+    if (head_dim != 64 && head_dim != 128)
+        return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: head_dim must be 64 or 128");
+    if (rope_style < 0 || rope_style > 2) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: bad rope_style");
+    if (!rope_cos || !rope_sin) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: RoPE tables are NULL");
+
+    pqa_ctx* c = new pqa_ctx();
+    c->n_layers = n_layers;
+    c->max_seq_len = max_seq_len;
+    c->n_heads = n_heads;
+    c->n_kv_heads = n_kv_heads;
+    c->head_dim = head_dim;
+    c->rope_style = rope_style;
+    c->kv_mul = n_heads / n_kv_heads;
+    c->n_chunk = (c->kv_mul + 7) / 8;
+    c->chunk_heads = (c->kv_mul + c->n_chunk - 1) / c->n_chunk;
+    c->q_dim = (size_t)n_heads * head_dim;
+    c->kv_dim = (size_t)n_kv_heads * head_dim;
+    c->layer_elems = (size_t)max_seq_len * c->kv_dim;
+    c->has_qk_norm.assign(n_layers, 0);
+
+    int rc = PQA_OK;
+    auto chk = [&](hipError_t e, const char* what) {
+        if (rc == PQA_OK && e != hipSuccess) {
+            const int code = e == hipErrorOutOfMemory ? PQA_ERR_NOMEM : PQA_ERR_HIP;
+            rc = set_err(nullptr, code, std::string("pqa_create: ") + what + ": " + hipGetErrorString(e));
+        }
+        return rc == PQA_OK;
+    };
+    if (chk(hipGetDevice(&c->device), "hipGetDevice")) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess && cus > 0)
+            c->cu_count = cus;
+    }
+    chk(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream");
+    const size_t cache = (size_t)n_layers * c->layer_elems;
+    const size_t half = (size_t)head_dim / 2;
+    const int ny = n_kv_heads * c->n_chunk;
+    c->max_splits = 256;
+    if (chk(dev_alloc(&c->key_cache, cache), "key cache") && chk(dev_alloc(&c->val_cache, cache), "value cache")) {
+        chk(hipMemset(c->key_cache, 0, cache * 2), "memset");
+        chk(hipMemset(c->val_cache, 0, cache * 2), "memset");
+    }
+    if (chk(dev_alloc(&c->rope_cos, (size_t)max_seq_len * half), "rope") &&
+        chk(dev_alloc(&c->rope_sin, (size_t)max_seq_len * half), "rope")) {
+        chk(hipMemcpy(c->rope_cos, rope_cos, (size_t)max_seq_len * half * 4, hipMemcpyHostToDevice), "rope copy");
+        chk(hipMemcpy(c->rope_sin, rope_sin, (size_t)max_seq_len * half * 4, hipMemcpyHostToDevice), "rope copy");
+    }
+    chk(dev_alloc(&c->qk_norm, (size_t)n_layers * 2 * head_dim), "qk norm");
+    chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
+    chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
+    if (chk(dev_alloc(&c->counters, (size_t)ny), "counters"))
+        chk(hipMemset(c->counters, 0, (size_t)ny * sizeof(unsigned)), "memset");
+    if (rc == PQA_OK) chk(hipDeviceSynchronize(), "sync");
+    if (rc != PQA_OK) {
+        free_ctx(c);
+        return rc;
+    }
+    *out = c;
+    return PQA_OK;
+}
+
+extern "C" void pqa_destroy(pqa_ctx* ctx) { free_ctx(ctx); }
+
+extern "C" const char* pqa_last_error(const pqa_ctx* ctx) {
+    return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+static int check_layer(pqa_ctx* ctx, int layer, const char* fn) {
+    if (layer < 0 || layer >= ctx->n_layers)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": layer out of range");
+    return PQA_OK;
+}
+
+extern "C" int pqa_set_qk_norm(pqa_ctx* ctx, int layer, const float* q_norm_w, const float* k_norm_w) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_qk_norm: ctx is NULL");
+    if (int rc = check_layer(ctx, layer, "pqa_set_qk_norm")) return rc;
+    if (!q_norm_w && !k_norm_w) {
+        ctx->has_qk_norm[layer] = 0;
+        return PQA_OK;
+    }
+    if (!q_norm_w || !k_norm_w)
+        return set_err(ctx, PQA_ERR_ARG, "pqa_set_qk_norm: give both weights or neither");
+    const size_t hd = (size_t)ctx->head_dim;
+    float* dst = ctx->qk_norm + (size_t)layer * 2 * hd;
+    if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_set_qk_norm")) return rc;
+    if (int rc = hip_check(ctx, hipMemcpy(dst, q_norm_w, hd * 4, hipMemcpyHostToDevice), "pqa_set_qk_norm"))
+        return rc;
+    if (int rc = hip_check(ctx, hipMemcpy(dst + hd, k_norm_w, hd * 4, hipMemcpyHostToDevice), "pqa_set_qk_norm"))
+        return rc;
+    ctx->has_qk_norm[layer] = 1;
+    return PQA_OK;
+}
+
+extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
+                          float* out) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_decode: ctx is NULL");
+    if (int rc = check_layer(ctx, layer, "pqa_decode")) return rc;
+    if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode: pos out of range");
+    if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: NULL buffer");
+    return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out), "pqa_decode");
+}
+
+static int ensure_q16(pqa_ctx* ctx, int n_tok) {
+    if ((size_t)n_tok <= ctx->q16_tokens) return PQA_OK;
+    if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_prefill")) return rc;
+    if (ctx->q16) (void)hipFree(ctx->q16);
+    ctx->q16 = nullptr;
+    ctx->q16_tokens = 0;
+    const size_t want = std::max<size_t>((size_t)n_tok, 256);
+    if (int rc = hip_check(ctx, dev_alloc(&ctx->q16, 2 * want * ctx->q_dim), "pqa_prefill: q staging")) return rc;
+    ctx->q16_tokens = want;
+    return PQA_OK;
+}
+
+extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q, const float* k,
+                           const float* v, float* out) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_prefill: ctx is NULL");
+    if (int rc = check_layer(ctx, layer, "pqa_prefill")) return rc;
+    if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: n_tok must be positive");
+    if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
+        return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill: positions out of range");
+    if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: NULL buffer");
+    if (int rc = ensure_q16(ctx, n_tok)) return rc;
+    return hip_check(ctx, pqa::launch_prefill(ctx, layer, start_pos, n_tok, q, k, v, out), "pqa_prefill");
+}
+
+static int ensure_stage(pqa_ctx* ctx, size_t floats) {
+    if (floats <= ctx->stage_floats) return PQA_OK;
+    if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "staging")) return rc;
+    if (ctx->stage) (void)hipFree(ctx->stage);
+    ctx->stage = nullptr;
+    ctx->stage_floats = 0;
+    if (int rc = hip_check(ctx, dev_alloc(&ctx->stage, floats), "staging")) return rc;
+    ctx->stage_floats = floats;
+    return PQA_OK;
+}
+
+static int run_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, const float* q, const float* k,
+                    const float* v, float* out, const char* fn) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
+    if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": NULL buffer");
+    if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": n_tok must be positive");
+    const size_t nq = (size_t)n_tok * ctx->q_dim, nkv = (size_t)n_tok * ctx->kv_dim;
+    if (int rc = ensure_stage(ctx, 2 * nq + 2 * nkv)) return rc;
+    float* dq = ctx->stage;
+    float* dk = dq + nq;
+    float* dv = dk + nkv;
+    float* dout = dv + nkv;
+    hipStream_t st = ctx->stream;
+    int rc = hip_check(ctx, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, st), fn);
+    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, st), fn);
+    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dv, v, nkv * 4, hipMemcpyHostToDevice, st), fn);
+    if (!rc)
+        rc = prefill ? pqa_prefill(ctx, layer, pos, n_tok, dq, dk, dv, dout)
+                     : pqa_decode(ctx, layer, pos, dq, dk, dv, dout);
+    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(out, dout, nq * 4, hipMemcpyDeviceToHost, st), fn);
+    if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
+    return rc;
+}
+
+extern "C" int pqa_decode_host(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
+                               float* out) {
+    return run_host(ctx, layer, pos, 1, false, q, k, v, out, "pqa_decode_host");
+}
+
+extern "C" int pqa_prefill_host(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q,
+                                const float* k, const float* v, float* out) {
+    return run_host(ctx, layer, start_pos, n_tok, true, q, k, v, out, "pqa_prefill_host");
+}
+
+static int kv_rows_check(pqa_ctx* ctx, int layer, int pos0, int n, const char* fn) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
+    if (int rc = check_layer(ctx, layer, fn)) return rc;
+    if (n < 0 || pos0 < 0 || (long long)pos0 + n > ctx->max_seq_len)
+        return set_err(ctx, PQA_ERR_RANGE, std::string(fn) + ": rows out of range");
+    return PQA_OK;
+}
+
+extern "C" int pqa_kv_upload(pqa_ctx* ctx, int layer, int pos0, int n, const uint16_t* k_rows,
+                             const uint16_t* v_rows) {
+    if (int rc = kv_rows_check(ctx, layer, pos0, n, "pqa_kv_upload")) return rc;
+    const size_t off = (size_t)layer * ctx->layer_elems + (size_t)pos0 * ctx->kv_dim;
+    const size_t bytes = (size_t)n * ctx->kv_dim * 2;
+    int rc = PQA_OK;
+    if (k_rows && bytes)
+        rc = hip_check(ctx, hipMemcpyAsync(ctx->key_cache + off, k_rows, bytes, hipMemcpyHostToDevice, ctx->stream),
+                       "pqa_kv_upload");
+    if (!rc && v_rows && bytes)
+        rc = hip_check(ctx, hipMemcpyAsync(ctx->val_cache + off, v_rows, bytes, hipMemcpyHostToDevice, ctx->stream),
+                       "pqa_kv_upload");
+    if (!rc) rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_kv_upload");
+    return rc;
+}
+
+extern "C" int pqa_kv_download(pqa_ctx* ctx, int layer, int pos0, int n, uint16_t* k_rows, uint16_t* v_rows) {
+    if (int rc = kv_rows_check(ctx, layer, pos0, n, "pqa_kv_download")) return rc;
+    const size_t off = (size_t)layer * ctx->layer_elems + (size_t)pos0 * ctx->kv_dim;
+    const size_t bytes = (size_t)n * ctx->kv_dim * 2;
+    int rc = PQA_OK;
+    if (k_rows && bytes)
+        rc = hip_check(ctx, hipMemcpyAsync(k_rows, ctx->key_cache + off, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                       "pqa_kv_download");
+    if (!rc && v_rows && bytes)
+        rc = hip_check(ctx, hipMemcpyAsync(v_rows, ctx->val_cache + off, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                       "pqa_kv_download");
+    if (!rc) rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_kv_download");
+    return rc;
+}
+
+extern "C" int pqa_kv_cache(pqa_ctx* ctx, uint16_t** key_cache, uint16_t** val_cache) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_kv_cache: ctx is NULL");
+    if (key_cache) *key_cache = ctx->key_cache;
+    if (val_cache) *val_cache = ctx->val_cache;
+    return PQA_OK;
+}
+
+extern "C" void* pqa_stream(pqa_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+extern "C" int pqa_sync(pqa_ctx* ctx) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_sync: ctx is NULL");
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_sync");
+}
+
+extern "C" void pqa_rope_table(float rope_base, int head_dim, int max_seq_len, float* cos_tab, float* sin_tab) {
+    const int half = head_dim / 2;
+    for (int pos = 0; pos < max_seq_len; pos++)
+        for (int i = 0; i < half; i++) {
+            const float theta = (float)pos / powf(rope_base, (float)(2 * i) / (float)head_dim);
+            cos_tab[(size_t)pos * half + i] = cosf(theta);
+            sin_tab[(size_t)pos * half + i] = sinf(theta);
+        }
+}
+
+extern "C" int pqa_fp32_to_fp16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_fp32_to_fp16: ctx is NULL");
+    if (n && (!src || !dst)) return set_err(ctx, PQA_ERR_ARG, "pqa_fp32_to_fp16: NULL buffer");
+    return hip_check(ctx, pqa::launch_f32_to_f16(ctx, src, dst, n), "pqa_fp32_to_fp16");
+}
+
+extern "C" int pqa_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float outlier_prob) {
+    if (int rc = kv_rows_check(ctx, layer, pos0, n, "pqa_synth_kv")) return rc;
+    return hip_check(ctx, pqa::launch_synth_kv(ctx, layer, pos0, n, seed, outlier_prob), "pqa_synth_kv");
+}
+
+extern "C" int pqa_set_decode_split(pqa_ctx* ctx, int rows_per_split) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_decode_split: ctx is NULL");
+    if (rows_per_split < 0 || (rows_per_split % 64) != 0)
+        return set_err(ctx, PQA_ERR_ARG, "pqa_set_decode_split: must be 0 or a positive multiple of 64");
+    ctx->split_override = rows_per_split;
+    return PQA_OK;
+}
+
+extern "C" int pqa_set_prefill_precision(pqa_ctx* ctx, int split_q) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_prefill_precision: ctx is NULL");
+    if (split_q != 0 && split_q != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_prefill_precision: 0 or 1");
+    ctx->prefill_split_q = split_q;
+    return PQA_OK;
+}

@@ -1,0 +1,120 @@
+// Device-side building blocks shared by the decode and prefill kernels:
+// the reference's fp16 rounding, its per-head RMSNorm reduction order and the
+// three RoPE pairings. Everything that feeds a K row written to the cache is
+// evaluated without FMA contraction so the fp16 bits match the reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pqa {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> fp16 exactly as cpp/quant.hpp:102-135 rounds: the magnitude gets
+// half an fp16 ulp added and is truncated (nearest, ties away from zero).
+// Normal range: adding 0x1000 to the rebased magnitude lets a mantissa carry
+// ripple into the exponent, and exponent 31 with a zero mantissa is the
+// infinity the reference returns. fp32 zero/subnormal -> signed zero;
+// NaN -> sign|0x7E00.
+__device__ __forceinline__ uint16_t f32_to_f16_ref(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t be = (bits >> 23) & 0xFFu;
+    const uint32_t mant = bits & 0x7FFFFFu;
+    uint32_t h;
+    if (be >= 143u) {
+        h = (be == 255u && mant) ? 0x7E00u : 0x7C00u;
+    } else if (be >= 113u) {
+        h = ((bits & 0x7FFFFFFFu) - (112u << 23) + 0x1000u) >> 13;
+    } else if (be >= 102u) {
+        const uint32_t shift = 126u - be;
+        h = ((mant | 0x800000u) + (1u << (shift - 1u))) >> shift;
+    } else {
+        h = 0u;
+    }
+    return (uint16_t)(sign | h);
+}
+
+// fp16 bits -> fp32: exact widening (the hardware conversion equals
+// cpp/quant.hpp:73-100 for every input, subnormals included).
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Inverse RMS of one head the way cpp/tensor.hpp:146-176 computes it on x86:
+// four SSE lane sums (lane j takes x[i] for i = j mod 4 while i+3 < n, in
+// increasing i), horizontal sum (l0+l2)+(l1+l3) (cpp/quant.hpp:296-302),
+// scalar tail, then 1/sqrt(ss/n + 1e-6). Called by one thread per head.
+__device__ __forceinline__ float rms_scale_ref(const float* x, int n) {
+#pragma clang fp contract(off)
+    float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
+    int i = 0;
+    for (; i + 3 < n; i += 4) {
+        l0 = l0 + x[i] * x[i];
+        l1 = l1 + x[i + 1] * x[i + 1];
+        l2 = l2 + x[i + 2] * x[i + 2];
+        l3 = l3 + x[i + 3] * x[i + 3];
+    }
+    float ss = (l0 + l2) + (l1 + l3);
+    for (; i < n; i++) ss = ss + x[i] * x[i];
+    return 1.0f / sqrtf(ss / (float)n + 1e-6f);
+}
+
+// Same reduction split over the 4 lanes of a quad (lane j owns SSE lane j);
+// every lane of the quad returns the scale. The lane sums are sequential in
+// i exactly as above; the quad exchange only moves finished values.
+// Must be called by all 4 lanes of the quad together.
+__device__ __forceinline__ float rms_scale_ref_quad(const float* x, int n, int j) {
+#pragma clang fp contract(off)
+    float l = 0.0f;
+    const int nfull = n & ~3;
+    for (int i = j; i < nfull; i += 4) l = l + x[i] * x[i];
+    const float L0 = __shfl(l, 0, 4), L1 = __shfl(l, 1, 4);
+    const float L2 = __shfl(l, 2, 4), L3 = __shfl(l, 3, 4);
+    float ss = (L0 + L2) + (L1 + L3);
+    for (int i = nfull; i < n; i++) ss = ss + x[i] * x[i];
+    return 1.0f / sqrtf(ss / (float)n + 1e-6f);
+}
+
+// Element indices of RoPE pair p (0 <= p < hd/2) for each pairing; the angle
+// is always p. Block8: full blocks of 4 pairs (4b+3 < half) pair 8b+j with
+// 8b+4+j (j = p mod 4); pairs past the last full block use the interleaved
+// tail (cpp/tensor.hpp:316-323).
+__device__ __forceinline__ void rope_pair(int style, int p, int hd, int& e0, int& e1) {
+    const int half = hd >> 1;
+    if (style == 0) {
+        e0 = p;
+        e1 = p + half;
+    } else if (style == 1 && (p | 3) < half) {
+        e0 = ((p >> 2) << 3) + (p & 3);
+        e1 = e0 + 4;
+    } else {
+        e0 = 2 * p;
+        e1 = 2 * p + 1;
+    }
+}
+
+// x' = x0*c - x1*s, y' = x0*s + x1*c with separate roundings (no FMA), as the
+// SSE and scalar code of cpp/tensor.hpp does.
+__device__ __forceinline__ void rope_rotate(float& x0, float& x1, float c, float s) {
+#pragma clang fp contract(off)
+    const float a = x0, b = x1;
+    x0 = a * c - b * s;
+    x1 = a * s + b * c;
+}
+
+// (x * s) * w, rounded twice (cpp/tensor.hpp:168-171).
+__device__ __forceinline__ float rms_apply(float x, float s, float w) {
+#pragma clang fp contract(off)
+    return (x * s) * w;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace pqa

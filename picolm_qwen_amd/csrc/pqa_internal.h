@@ -1,0 +1,63 @@
+// Context layout and kernel launchers of the attention backend (host side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "pqa.h"
+
+struct pqa_ctx {
+    int n_layers = 0, max_seq_len = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, rope_style = 0;
+    int kv_mul = 1;            // query heads per KV head (cpp/model.hpp:295)
+    int n_chunk = 1, chunk_heads = 1;  // query heads of one KV head split into chunks of <= 8
+    size_t q_dim = 0, kv_dim = 0;
+    size_t layer_elems = 0;    // max_seq_len * kv_dim
+
+    uint16_t* key_cache = nullptr;  // [n_layers][max_seq_len][kv_dim]
+    uint16_t* val_cache = nullptr;
+    float* rope_cos = nullptr;      // [max_seq_len][head_dim/2]
+    float* rope_sin = nullptr;
+    float* qk_norm = nullptr;       // [n_layers][2][head_dim]
+    std::vector<char> has_qk_norm;
+
+    // decode split-K workspace
+    float* part_acc = nullptr;      // [n_kv*n_chunk][max_splits][chunk_heads][head_dim]
+    float* part_ml = nullptr;       // [n_kv*n_chunk][max_splits][chunk_heads][2]
+    unsigned* counters = nullptr;   // [n_kv*n_chunk], zero between calls
+    int max_splits = 0;
+    int split_override = 0;
+    int cu_count = 256;
+
+    // prefill: normed, roped, scaled q in fp16, [tokens][n_heads][head_dim],
+    // followed by the same-sized low part when prefill_split_q is set
+    _Float16* q16 = nullptr;
+    size_t q16_tokens = 0;
+    int prefill_split_q = 0;
+
+    // staging for the _host entry points
+    float* stage = nullptr;
+    size_t stage_floats = 0;
+
+    hipStream_t stream = nullptr;
+    int device = 0;
+    std::string err;
+};
+
+namespace pqa {
+
+int set_err(pqa_ctx* ctx, int code, const std::string& msg);
+int hip_check(pqa_ctx* ctx, hipError_t e, const char* what);
+
+// Rows per decode workgroup and the number of splits for `hist` history rows.
+void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit);
+
+hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
+                         const float* v, float* out);
+hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
+                          const float* k, const float* v, float* out);
+hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
+hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
+
+}  // namespace pqa

@@ -1,0 +1,347 @@
+// Causal prefill of one layer: the token loop of cpp/model.hpp:493-593 as two
+// launches.
+//
+// 1. prefill_prep: one workgroup per token. QK-RMSNorm (reference reduction
+//    order), RoPE at the token's position, K and V rounded to fp16 with the
+//    reference's rounding into cache rows start..start+n-1, and q scaled by
+//    log2(e)/sqrt(hd) and rounded to fp16 for the MFMA stage.
+// 2. prefill_attn: flash attention over the fp16 cache on
+//    v_mfma_f32_32x32x16_f16. The query heads of one KV head are packed as
+//    rows R = token*g + h (g = query heads per KV head), so one K/V tile in
+//    LDS serves the whole GQA group. A workgroup is 4 waves x 32 packed rows;
+//    per 64-key tile each wave computes S^T = K Q^T (keys x rows), the online
+//    softmax per row (a lane owns one row: its 32 scores plus the partner
+//    lane 32 apart), and O^T += V^T P^T. With S^T in the MFMA result layout the
+//    lane's scores are already the B operand of the PV product, so P never
+//    leaves registers. V is stored transposed in LDS. Tiles past the causal
+//    limit of every row in a wave are skipped. Workgroup blockIdx.x runs
+//    query block nblk-1-x and then block x, so each workgroup does about the
+//    same causal work.
+#include "pqa_device.h"
+#include "pqa_internal.h"
+
+namespace pqa {
+
+struct PrepArgs {
+    const float* q;  // [n_tok][nh*HD]
+    const float* k;  // [n_tok][kv_dim]
+    const float* v;
+    const float* qn;
+    const float* kn;
+    const float* cos_tab;  // [S][HD/2]
+    const float* sin_tab;
+    uint16_t* kc;
+    uint16_t* vc;
+    _Float16* q16;     // [n_tok][nh][HD], fp16(q * qscale)
+    _Float16* q16_lo;  // null, or the rounding residual fp16(q*qscale - q16)
+    int start, nh, nkv, rope;
+    float qscale;
+};
+
+constexpr int kPrepThreads = 256;
+
+template <int HD>
+__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(const PrepArgs a) {
+    extern __shared__ float sx[];  // [(nh + nkv) * HD] then [nh + nkv] scales
+    const int tid = threadIdx.x;
+    const int tok = blockIdx.x;
+    const int pos = a.start + tok;
+    const int nheads = a.nh + a.nkv;
+    const size_t q_dim = (size_t)a.nh * HD, kv_dim = (size_t)a.nkv * HD;
+    float* scale = sx + (size_t)nheads * HD;
+
+    for (int i = tid; i < nheads * HD; i += kPrepThreads)
+        sx[i] = i < (int)q_dim ? a.q[tok * q_dim + i] : a.k[tok * kv_dim + (i - q_dim)];
+    __syncthreads();
+    if (a.qn) {
+        for (int base = 0; base < nheads; base += kPrepThreads / 4) {
+            const int hh = base + (tid >> 2);
+            if (hh < nheads) scale[hh] = rms_scale_ref_quad(sx + (size_t)hh * HD, HD, tid & 3);
+        }
+        __syncthreads();
+        for (int i = tid; i < nheads * HD; i += kPrepThreads) {
+            const int hh = i / HD, d = i - (i / HD) * HD;
+            sx[i] = rms_apply(sx[i], scale[hh], hh < a.nh ? a.qn[d] : a.kn[d]);
+        }
+        __syncthreads();
+    }
+    constexpr int HALF = HD / 2;
+    const float* c = a.cos_tab + (size_t)pos * HALF;
+    const float* s = a.sin_tab + (size_t)pos * HALF;
+    for (int i = tid; i < nheads * HALF; i += kPrepThreads) {
+        const int hh = i / HALF, p = i - (i / HALF) * HALF;
+        int e0, e1;
+        rope_pair(a.rope, p, HD, e0, e1);
+        float* x = sx + (size_t)hh * HD;
+        rope_rotate(x[e0], x[e1], c[p], s[p]);
+    }
+    __syncthreads();
+    uint16_t* krow = a.kc + (size_t)pos * kv_dim;
+    uint16_t* vrow = a.vc + (size_t)pos * kv_dim;
+    for (int i = tid; i < (int)kv_dim; i += kPrepThreads) {
+        krow[i] = f32_to_f16_ref(sx[q_dim + i]);
+        vrow[i] = f32_to_f16_ref(a.v[tok * kv_dim + i]);
+    }
+    _Float16* qrow = a.q16 + tok * q_dim;
+    _Float16* qlo = a.q16_lo ? a.q16_lo + tok * q_dim : nullptr;
+    for (int i = tid; i < (int)q_dim; i += kPrepThreads) {
+        const float x = sx[i] * a.qscale;
+        const _Float16 hi = (_Float16)x;
+        qrow[i] = hi;
+        if (qlo) qlo[i] = (_Float16)(x - (float)hi);
+    }
+}
+
+struct AttnArgs {
+    const _Float16* q16;
+    const _Float16* q16_lo;  // used when SPLITQ
+    const uint16_t* kc;
+    const uint16_t* vc;
+    float* out;
+    int start, n_tok, nh, g, kv_dim, rows, nblk;
+};
+
+constexpr int kAttnThreads = 256;
+constexpr int kRowsPerBlock = 128;
+constexpr int kKeysPerTile = 64;
+
+template <int HD>
+struct AttnTile {
+    static constexpr int KST = HD + 8;              // K row stride in LDS (halves)
+    static constexpr int VST = kKeysPerTile + 4;    // V^T row stride (halves)
+    static constexpr int KCH = kKeysPerTile * HD / 8 / kAttnThreads;  // 16-B K chunks per thread
+    static constexpr int VCH = KCH;
+    static constexpr int DBLK = HD / 8;             // 16-B chunks per row
+};
+
+// SPLITQ: scores use q = hi + lo (two fp16 MFMAs into one fp32 accumulator),
+// which keeps fp32-level score precision when keys carry large outliers.
+template <int HD, bool SPLITQ>
+__global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const AttnArgs a) {
+    using T = AttnTile<HD>;
+    constexpr int QK = HD / 16;   // k-steps of S^T = K Q^T
+    constexpr int DT = HD / 32;   // 32-dim tiles of O^T
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    __shared__ __attribute__((aligned(16))) _Float16 sK[kKeysPerTile * T::KST];
+    __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * T::VST];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int col = lane & 31;   // q row within the wave / MFMA row index
+    const int hk = lane >> 5;    // MFMA k-group
+    const int kvh = blockIdx.y;
+    const uint16_t* kbase = a.kc + (size_t)kvh * HD;
+    const uint16_t* vbase = a.vc + (size_t)kvh * HD;
+
+    const int b_first = a.nblk - 1 - (int)blockIdx.x;
+    const int b_second = (int)blockIdx.x;
+    for (int pass = 0; pass < 2; pass++) {
+        const int b = pass == 0 ? b_first : b_second;
+        if (pass == 1 && b_second >= b_first) break;
+
+        const int R0 = b * kRowsPerBlock + w * 32;
+        const int R = R0 + col;
+        const bool rvalid = R < a.rows;
+        const int tok = rvalid ? R / a.g : 0;
+        const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
+        const int qpos = a.start + tok;
+
+        half8 qf[QK], qfl[SPLITQ ? QK : 1];
+        {
+            const size_t qoff = ((size_t)tok * a.nh + hq) * HD + 8 * hk;
+#pragma unroll
+            for (int ks = 0; ks < QK; ks++) {
+                const u32x4 raw = rvalid ? *(const u32x4*)(a.q16 + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+                qf[ks] = __builtin_bit_cast(half8, raw);
+                if constexpr (SPLITQ) {
+                    const u32x4 rl = rvalid ? *(const u32x4*)(a.q16_lo + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+                    qfl[ks] = __builtin_bit_cast(half8, rl);
+                }
+            }
+        }
+        const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
+        const int kend = a.start + last_row_blk / a.g + 1;
+        const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
+        const int kend_w = R0 < a.rows ? a.start + (min(a.rows, R0 + 32) - 1) / a.g + 1 : 0;
+        const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
+
+        float m_run = NEG_INF, l_run = 0.0f;
+        floatx16 o[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+
+        // global -> register staging of one K/V tile
+        u32x4 kreg[T::KCH], vreg[T::VCH];
+        auto gload = [&](int key0) {
+#pragma unroll
+            for (int j = 0; j < T::KCH; j++) {
+                const int c = tid + j * kAttnThreads;
+                const int key = min(key0 + c / T::DBLK, kend - 1);
+                kreg[j] = *(const u32x4*)(kbase + (size_t)key * a.kv_dim + 8 * (c % T::DBLK));
+            }
+#pragma unroll
+            for (int j = 0; j < T::VCH; j++) {
+                const int key = min(key0 + (tid & 63), kend - 1);
+                const int dblk = (tid >> 6) + 4 * j;
+                vreg[j] = *(const u32x4*)(vbase + (size_t)key * a.kv_dim + 8 * dblk);
+            }
+        };
+        auto lds_store = [&]() {
+#pragma unroll
+            for (int j = 0; j < T::KCH; j++) {
+                const int c = tid + j * kAttnThreads;
+                *(u32x4*)(sK + (c / T::DBLK) * T::KST + 8 * (c % T::DBLK)) = kreg[j];
+            }
+#pragma unroll
+            for (int j = 0; j < T::VCH; j++) {
+                const int kk = tid & 63;
+                const int dblk = (tid >> 6) + 4 * j;
+                const half8 vv = __builtin_bit_cast(half8, vreg[j]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) sVt[(8 * dblk + e) * T::VST + kk] = vv[e];
+            }
+        };
+
+        gload(0);
+        for (int kt = 0; kt < ntiles; kt++) {
+            const int key0 = kt * kKeysPerTile;
+            __syncthreads();  // previous tile's LDS reads are done
+            lds_store();
+            __syncthreads();
+            if (kt + 1 < ntiles) gload(key0 + kKeysPerTile);
+            if (key0 >= kend_w) continue;  // wave-uniform: every row of this wave is done
+
+            floatx16 sacc[2];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) sacc[t2][r] = 0.0f;
+                const _Float16* kp = sK + (32 * t2 + col) * T::KST + 8 * hk;
+#pragma unroll
+                for (int ks = 0; ks < QK; ks++) {
+                    const half8 kf = *(const half8*)(kp + 16 * ks);
+                    sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sacc[t2], 0, 0, 0);
+                    if constexpr (SPLITQ)
+                        sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfl[ks], sacc[t2], 0, 0, 0);
+                }
+            }
+            // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
+            if (key0 + kKeysPerTile - 1 > qpos_min_w) {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
+                        if (key > qpos) sacc[t2][r] = NEG_INF;
+                    }
+            }
+            float mx = NEG_INF;
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m_run, mx);
+            const float corr = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            float psum = 0.0f;
+            half8 pf[4];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float p = fast_exp2(sacc[t2][r] - m_new);
+                    psum += p;
+                    pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)p;
+                }
+            l_run = l_run * corr + psum;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const _Float16* vp = sVt + (32 * dt + col) * T::VST + 16 * s + 4 * hk;
+                    const u32x2 lo = *(const u32x2*)vp;
+                    const u32x2 hi = *(const u32x2*)(vp + 8);
+                    const u32x4 raw = {lo[0], lo[1], hi[0], hi[1]};
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, raw), pf[s],
+                                                                   o[dt], 0, 0, 0);
+                }
+            }
+        }
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        if (rvalid) {
+            const float inv = 1.0f / l_tot;
+            float* op = a.out + ((size_t)tok * a.nh + hq) * HD + 4 * hk;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; r4++) {
+                    floatx4 vv = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                                  o[dt][4 * r4 + 3] * inv};
+                    *(floatx4*)(op + 32 * dt + 8 * r4) = vv;
+                }
+        }
+    }
+}
+
+template <int HD>
+static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
+                                    const float* k, const float* v, float* out) {
+    PrepArgs p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    const bool norm = ctx->has_qk_norm[layer] != 0;
+    p.qn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD : nullptr;
+    p.kn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD + HD : nullptr;
+    p.cos_tab = ctx->rope_cos;
+    p.sin_tab = ctx->rope_sin;
+    p.kc = ctx->key_cache + (size_t)layer * ctx->layer_elems;
+    p.vc = ctx->val_cache + (size_t)layer * ctx->layer_elems;
+    const bool splitq = ctx->prefill_split_q != 0;
+    p.q16 = ctx->q16;
+    p.q16_lo = splitq ? ctx->q16 + (size_t)n_tok * ctx->q_dim : nullptr;
+    p.start = start;
+    p.nh = ctx->n_heads;
+    p.nkv = ctx->n_kv_heads;
+    p.rope = ctx->rope_style;
+    p.qscale = 1.4426950408889634f / sqrtf((float)HD);
+    const size_t shm = ((size_t)(ctx->n_heads + ctx->n_kv_heads) * (HD + 1)) * sizeof(float);
+    hipLaunchKernelGGL(prefill_prep_kernel<HD>, dim3(n_tok), dim3(kPrepThreads), shm, ctx->stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+
+    AttnArgs a;
+    a.q16 = ctx->q16;
+    a.q16_lo = p.q16_lo;
+    a.kc = p.kc;
+    a.vc = p.vc;
+    a.out = out;
+    a.start = start;
+    a.n_tok = n_tok;
+    a.nh = ctx->n_heads;
+    a.g = ctx->kv_mul;
+    a.kv_dim = (int)ctx->kv_dim;
+    a.rows = n_tok * ctx->kv_mul;
+    a.nblk = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    dim3 grid((a.nblk + 1) / 2, ctx->n_kv_heads);
+    if (splitq) hipLaunchKernelGGL((prefill_attn_kernel<HD, true>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<HD, false>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
+                          const float* k, const float* v, float* out) {
+    if (ctx->head_dim == 64) return launch_prefill_hd<64>(ctx, layer, start, n_tok, q, k, v, out);
+    if (ctx->head_dim == 128) return launch_prefill_hd<128>(ctx, layer, start, n_tok, q, k, v, out);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace pqa

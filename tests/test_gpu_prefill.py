@@ -1,0 +1,94 @@
+"""Prefill parity on the GPU: causal MFMA flash attention and the batched
+append against the oracle's token loop (cpp/model.hpp:493-593)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import cpu_threads
+from gpu_util import assert_bits_equal, assert_close
+
+torch = pytest.importorskip("torch")
+from picolm_qwen_amd import PicoAttention  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+# name, n_heads, n_kv, head_dim, max_seq_len, rope_style, rope_base, qk_norm, start, n_tok, history_outliers
+# Cases whose history has x8 outlier rows run with the split-q precision mode:
+# a single fp16 rounding of q moves those scores by ~1e-2 (see pqa.h).
+CASES = [
+    ("qwen3_4b_s256", 32, 8, 128, 256, 0, 1e6, True, 0, 256, 0.0),
+    ("qwen3_4b_start37_n200", 32, 8, 128, 512, 0, 1e6, True, 37, 200, 0.0),
+    ("tinyllama_block8_n1", 32, 4, 64, 64, 1, 1e4, False, 0, 1, 0.0),
+    ("tinyllama_block8_n129", 32, 4, 64, 256, 1, 1e4, False, 5, 129, 0.0),
+    ("qwen25_g7_n100", 14, 2, 64, 512, 0, 1e6, False, 300, 100, 0.01),
+    ("g2_n77", 16, 8, 128, 128, 0, 1e6, True, 0, 77, 0.0),
+    ("g16_n40", 32, 2, 128, 128, 2, 1e4, True, 10, 40, 0.0),
+    ("g1_interleaved_n65", 4, 4, 64, 96, 2, 1e4, False, 0, 65, 0.0),
+]
+
+
+def _prefill_case(idx, nh, nkv, hd, smax, style, base, qk, start, n_tok, prob, split_q=False):
+    seed = 9000 + idx
+    kvd = nkv * hd
+    cos, sin = O.rope_table(base, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, style, rope_cos=cos, rope_sin=sin)
+    att.set_prefill_precision(prob > 0 or split_q)
+    qn = kn = None
+    if qk:
+        qn, kn = O.qk_norm_weights(seed, 0, hd)
+        att.set_qk_norm(0, qn, kn)
+    kc = np.zeros((smax, kvd), np.uint16)
+    vc = np.zeros((smax, kvd), np.uint16)
+    if start:
+        att.synth_kv(0, 0, start, seed, prob)
+        kc[:start], vc[:start] = O.synth_kv_rows(seed, 0, kvd, 0, start, prob, cpu_threads())
+    q, k, v = O.batch_inputs(seed, 0, 0, n_tok, nh, nkv, hd)
+    dev = torch.device("cuda:0")
+    out = att.forward_batch(0, start, *(torch.from_numpy(x).to(dev) for x in (q, k, v)))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    shp = O.shape(nh, nkv, hd, smax, style)
+    want = O.prefill(shp, start, q, k, v, qn, kn, cos, sin, kc, vc, serial=False, n_threads=cpu_threads())
+    gk, gv = att.kv_download(0, start, n_tok)
+    assert_bits_equal(gk, kc[start:start + n_tok], "appended K rows")
+    assert_bits_equal(gv, vc[start:start + n_tok], "appended V rows")
+    err = assert_close(got, want)
+    att.close()
+    return err
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_prefill_matches_oracle(case):
+    print(f"prefill case {case[0]}", flush=True)
+    _prefill_case(CASES.index(case), *case[1:])
+
+
+def test_prefill_split_q_mode_on_plain_inputs():
+    print("prefill split-q mode", flush=True)
+    _prefill_case(40, 32, 8, 128, 300, 0, 1e6, True, 20, 250, 0.0, split_q=True)
+
+
+def test_prefill_row_equals_decode():
+    # causal prefill row i == decode at pos start+i over the same cache
+    nh, nkv, hd, smax, n = 16, 8, 128, 256, 150
+    cos, sin = O.rope_table(1e6, hd, smax)
+    qn, kn = O.qk_norm_weights(3, 0, hd)
+    q, k, v = O.batch_inputs(3, 0, 0, n, nh, nkv, hd)
+    dev = torch.device("cuda:0")
+    a = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    a.set_qk_norm(0, qn, kn)
+    pre = a.forward_batch(0, 0, *(torch.from_numpy(x).to(dev) for x in (q, k, v)))
+    b = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    b.set_qk_norm(0, qn, kn)
+    dec = []
+    for i in range(n):
+        dec.append(b.forward(0, i, q[i], k[i], v[i]))
+    torch.cuda.synchronize()
+    pre = pre.cpu().numpy()
+    assert_close(pre, np.stack(dec), atol=2e-3, rtol=1e-2, what="prefill vs decode")
+    ka, va = a.kv_download(0, 0, n)
+    kb, vb = b.kv_download(0, 0, n)
+    assert_bits_equal(ka, kb, "K rows prefill vs decode")
+    assert_bits_equal(va, vb, "V rows prefill vs decode")
+    a.close()
+    b.close()
