@@ -1,0 +1,331 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention path on one MI355X.
+
+Headline (`value`): decode attention of a Qwen3-8B-shaped model (32 query /
+8 KV heads, head_dim 128, QK-RMSNorm, NeoX RoPE theta 1e6), one token at
+position 131071 over a 131072-entry fp16 KV cache, all 36 layers per step
+(19.3 GB of cache rotated through, so the 256 MB Infinity Cache cannot hold
+it), 1 % of history rows scaled x8. Unit: algorithmic KV GB/s = bytes the
+reference reads and writes per layer (K and V rows 0..pos, q, k, v, out, the
+appended row) / time.
+
+Also reported in the same JSON line under "workloads":
+  qwen3_1.7b_decode   16/8/128, pos 32767, 28 layers (HBM-bound)
+  qwen3_4b_prefill    32/8/128, 2048-token causal prefill, 36 layers (MFMA)
+  tinyllama_decode    32/4/64, block8 RoPE, pos 511, 1 layer (latency)
+  qwen2.5_0.5b_sweep  14/2/64, positions 0..4095 token by token, 24 layers
+
+`roofline` covers the decode kernel of the headline workload, timed with HIP
+events on the library's stream. `cpu_baseline` times the CPU oracle (the
+reference loop restated, heads split over T threads) on one layer of the same
+cache, downloaded from the GPU.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2516.6  # dense fp16, 256 CU x 2.4 GHz x 4096 flop/clk
+METRIC = "attn µs/layer; decode KV GB/s (% HBM peak); prefill TFLOP/s (% MFMA)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(ctx, nh, nkv, hd):
+    """Algorithmic bytes of one decode launch: K and V rows 0..pos read
+    (ctx rows), q/k/v fp32 in, out fp32, the new K/V row written."""
+    kv_dim = nkv * hd
+    return 2 * ctx * kv_dim * 2 + nh * hd * 4 + 2 * kv_dim * 4 + nh * hd * 4 + 2 * kv_dim * 2
+
+
+def prefill_flops(nh, hd, s, start=0):
+    """Causal attention flops: 2 matmuls x 2 flop x n_q x hd x (key count summed over rows)."""
+    keys = sum(start + i + 1 for i in range(s))
+    return 2 * 2 * nh * hd * keys
+
+
+class Ctx:
+    """Thin ctypes holder around one pqa context (the bench calls the C ABI directly)."""
+
+    def __init__(self, n_layers, smax, nh, nkv, hd, style, base):
+        from picolm_qwen_amd import _lib
+        from picolm_qwen_amd.attention import rope_table
+        self.L = _lib.lib()
+        self.check = _lib.check
+        cos, sin = rope_table(base, hd, smax)
+        h = C.c_void_p()
+        self.check(self.L.pqa_create(C.byref(h), n_layers, smax, nh, nkv, hd, style,
+                                     cos.ctypes.data_as(C.c_void_p), sin.ctypes.data_as(C.c_void_p)))
+        self.h = h
+        self.n_layers, self.smax, self.nh, self.nkv, self.hd = n_layers, smax, nh, nkv, hd
+
+    def stream(self):
+        return self.L.pqa_stream(self.h)
+
+    def close(self):
+        if self.h:
+            self.L.pqa_destroy(self.h)
+            self.h = None
+
+
+def make_inputs(torch, dev, rng, n_layers, n_tok, nh, nkv, hd):
+    q = torch.from_numpy(rng.standard_normal((n_layers, n_tok, nh * hd), dtype=np.float32)).to(dev)
+    k = torch.from_numpy(rng.standard_normal((n_layers, n_tok, nkv * hd), dtype=np.float32)).to(dev)
+    v = torch.from_numpy(rng.standard_normal((n_layers, n_tok, nkv * hd), dtype=np.float32)).to(dev)
+    out = torch.empty((n_layers, n_tok, nh * hd), dtype=torch.float32, device=dev)
+    return q, k, v, out
+
+
+def set_norms(cx, rng, hd):
+    for layer in range(cx.n_layers):
+        qw = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+        kw = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+        cx.check(cx.L.pqa_set_qk_norm(cx.h, layer, qw.ctypes.data_as(C.c_void_p),
+                                      kw.ctypes.data_as(C.c_void_p)), cx.h)
+    return
+
+
+def timed(torch, cx, fn, steps, warmup):
+    """Runs fn() warmup+steps times; returns (wall ms/step, event ms/step on the library stream)."""
+    ext = torch.cuda.ExternalStream(cx.stream())
+    for _ in range(warmup):
+        fn()
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(ext)
+    for _ in range(steps):
+        fn()
+    e1.record(ext)
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, e0.elapsed_time(e1) / steps
+
+
+def decode_workload(torch, dev, name, n_layers, nh, nkv, hd, style, base, pos, prob, steps, warmup, qk_norm,
+                    seed=20251201, keep=False):
+    cx = Ctx(n_layers, pos + 1, nh, nkv, hd, style, base)
+    rng = np.random.default_rng(seed)
+    if qk_norm:
+        set_norms(cx, rng, hd)
+    for layer in range(n_layers):
+        cx.check(cx.L.pqa_synth_kv(cx.h, layer, 0, pos, seed, prob), cx.h)
+    q, k, v, out = make_inputs(torch, dev, rng, n_layers, 1, nh, nkv, hd)
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    torch.cuda.synchronize()
+    ptr = lambda t, layer: C.c_void_p(t[layer].data_ptr())  # noqa: E731
+    args = [(layer, ptr(q, layer), ptr(k, layer), ptr(v, layer), ptr(out, layer)) for layer in range(n_layers)]
+    dec = cx.L.pqa_decode
+    h = cx.h
+
+    def step():
+        for layer, a, b, c, d in args:
+            dec(h, layer, pos, a, b, c, d)
+
+    wall, ev = timed(torch, cx, step, steps, warmup)
+    per_layer_us = ev * 1e3 / n_layers
+    nbytes = decode_bytes(pos + 1, nh, nkv, hd)
+    gbs = nbytes / (per_layer_us * 1e-6) / 1e9
+    res = {"workload": name, "n_layers": n_layers, "pos": pos, "us_per_layer": round(per_layer_us, 3),
+           "bytes_per_layer": nbytes, "GB_per_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "ms_per_step_event": round(ev, 4), "ms_per_step_wall": round(wall, 4)}
+    log(f"[bench] {name}: {per_layer_us:.2f} us/layer, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+    if keep:
+        return res, cx, (q, k, v, out)
+    cx.close()
+    return res, None, None
+
+
+def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4242):
+    cx = Ctx(n_layers, s, nh, nkv, hd, 0, 1e6)
+    rng = np.random.default_rng(seed)
+    set_norms(cx, rng, hd)
+    q, k, v, out = make_inputs(torch, dev, rng, n_layers, s, nh, nkv, hd)
+    torch.cuda.synchronize()
+    ptr = lambda t, layer: C.c_void_p(t[layer].data_ptr())  # noqa: E731
+    args = [(layer, ptr(q, layer), ptr(k, layer), ptr(v, layer), ptr(out, layer)) for layer in range(n_layers)]
+    pre = cx.L.pqa_prefill
+    h = cx.h
+
+    def step():
+        for layer, a, b, c, d in args:
+            pre(h, layer, 0, s, a, b, c, d)
+
+    wall, ev = timed(torch, cx, step, steps, warmup)
+    per_layer_us = ev * 1e3 / n_layers
+    fl = prefill_flops(nh, hd, s)
+    tf = fl / (per_layer_us * 1e-6) / 1e12
+    res = {"workload": "qwen3_4b_prefill", "n_layers": n_layers, "n_tok": s,
+           "us_per_layer_append_plus_attention": round(per_layer_us, 3), "flops_per_layer": fl,
+           "TFLOP_per_s": round(tf, 1), "mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "dtype": "fp16",
+           "ms_per_step_event": round(ev, 4), "ms_per_step_wall": round(wall, 4)}
+    log(f"[bench] prefill: {per_layer_us:.2f} us/layer, {tf:.1f} TFLOP/s ({100 * tf / MFMA_FP16_PEAK_TFLOPS:.1f}% MFMA)")
+    cx.close()
+    return res
+
+
+def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096, checkpoints=(1, 512, 1024, 2048, 4096)):
+    cx = Ctx(n_layers, positions, nh, nkv, hd, 0, 1e6)
+    rng = np.random.default_rng(777)
+    q, k, v, out = make_inputs(torch, dev, rng, n_layers, positions, nh, nkv, hd)
+    torch.cuda.synchronize()
+    dec = cx.L.pqa_decode
+    h = cx.h
+    qp, kp, vp, op = (t.data_ptr() for t in (q, k, v, out))
+    qs, kvs = nh * hd * 4, nkv * hd * 4
+    ext = torch.cuda.ExternalStream(cx.stream())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(ext)
+    for pos in range(positions):
+        for layer in range(n_layers):
+            off_q = ((layer * positions) + pos)
+            dec(h, layer, pos, C.c_void_p(qp + off_q * qs), C.c_void_p(kp + off_q * kvs),
+                C.c_void_p(vp + off_q * kvs), C.c_void_p(op + off_q * qs))
+    e1.record(ext)
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    avg_us = e0.elapsed_time(e1) * 1e3 / (positions * n_layers)
+    curve = {}
+    for ctx_len in checkpoints:
+        pos = ctx_len - 1
+
+        def step():
+            for layer in range(n_layers):
+                off_q = ((layer * positions) + pos)
+                dec(h, layer, pos, C.c_void_p(qp + off_q * qs), C.c_void_p(kp + off_q * kvs),
+                    C.c_void_p(vp + off_q * kvs), C.c_void_p(op + off_q * qs))
+
+        _, ev = timed(torch, cx, step, 20, 2)
+        curve[str(ctx_len)] = round(ev * 1e3 / n_layers, 3)
+    cx.close()
+    log(f"[bench] qwen2.5 sweep: avg {avg_us:.2f} us/layer over ctx 1..{positions}; curve {curve}")
+    return {"workload": "qwen2.5_0.5b_sweep", "n_layers": n_layers, "positions": positions,
+            "avg_us_per_layer_launch_loop": round(avg_us, 3), "us_per_layer_vs_ctx": curve}
+
+
+def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
+    """The oracle (reference attention loop, restated in C) on layer 0 of the
+    headline cache: same K/V bytes (downloaded), same q/k/v and norm weights."""
+    import oracle as O
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    kv_dim = nkv * hd
+    smax = pos + 1
+    kc = np.zeros((smax, kv_dim), np.uint16)
+    vc = np.zeros((smax, kv_dim), np.uint16)
+    cx.check(cx.L.pqa_kv_download(cx.h, 0, 0, pos, kc.ctypes.data_as(C.c_void_p), vc.ctypes.data_as(C.c_void_p)), cx.h)
+    qn = np.empty(hd, np.float32)
+    kn = np.empty(hd, np.float32)
+    rng = np.random.default_rng(20251201)  # same draw order as decode_workload
+    for _ in range(1):
+        qn[:] = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+        kn[:] = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+    from picolm_qwen_amd.attention import rope_table
+    cos, sin = rope_table(1e6, hd, smax)
+    shp = O.shape(nh, nkv, hd, smax, 0)
+    qh, kh, vh = (t[0, 0].cpu().numpy() for t in (q, k, v))
+    t0 = time.perf_counter()
+    want = O.attn_step(shp, pos, qh, kh, vh, qn, kn, cos[pos], sin[pos], kc, vc, 1)
+    t1 = time.perf_counter() - t0
+    got = out0.cpu().numpy().reshape(-1)
+    max_err = float(np.abs(got - want).max())
+    log(f"[bench] layer-0 GPU output vs oracle: max abs err {max_err:.2e}")
+    reps, total = 0, 0.0
+    while total < budget_s and reps < 200:
+        t0 = time.perf_counter()
+        O.attn_step(shp, pos, qh, kh, vh, qn, kn, cos[pos], sin[pos], kc, vc, threads)
+        total += time.perf_counter() - t0
+        reps += 1
+    per_layer = total / reps
+    nbytes = decode_bytes(pos + 1, nh, nkv, hd)
+    log(f"[bench] cpu oracle: 1 thread {t1 * 1e6:.0f} us/layer, {threads} threads {per_layer * 1e6:.0f} us/layer")
+    return {"value": round(nbytes / per_layer / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": round(per_layer * 1e6, 1), "us_per_layer_1_thread": round(t1 * 1e6, 1),
+            "gpu_vs_oracle_max_abs_err": max_err,
+            "sample": f"layer 0 of 36 of the headline decode (pos {pos}, same cache bytes and inputs), "
+                      f"oracle attention step run {reps}x with query heads split over {threads} threads, "
+                      f"plus once on 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode would shard by KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+
+    nh, nkv, hd, layers, pos = 32, 8, 128, 36, 131071
+    head, cx, bufs = decode_workload(torch, dev, "qwen3_8b_decode", layers, nh, nkv, hd, 0, 1e6, pos, 0.01,
+                                     args.steps, args.warmup, True, keep=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cx, bufs[0], bufs[1], bufs[2], bufs[3][0, 0], nh, nkv, hd, pos)
+    cx.close()
+    del bufs
+    torch.cuda.empty_cache()
+
+    workloads = {"qwen3_8b_decode": head}
+    if not args.quick:
+        workloads["qwen3_1.7b_decode"] = decode_workload(torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6,
+                                                         32767, 0.0, args.steps, args.warmup, True)[0]
+        workloads["qwen3_4b_prefill"] = prefill_workload(torch, dev, 36, 32, 8, 128, 2048,
+                                                         max(3, args.steps // 5), 1)
+        workloads["tinyllama_decode"] = decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
+                                                        0.0, max(args.steps, 200), args.warmup, False)[0]
+        workloads["qwen2.5_0.5b_sweep"] = sweep_workload(torch, dev)
+
+    per_layer_us = head["us_per_layer"]
+    achieved = head["GB_per_s"]
+    line = {
+        "metric": METRIC,
+        "value": achieved,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step_event"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) q/k/v, cache history N(0,1) with 1% rows x8, fp16)",
+        "config": {"workload": "Qwen3-8B-shaped decode attention: 1 token at pos 131071 over a 131072-entry "
+                               "fp16 KV cache, all 36 layers per step",
+                   "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "layers": layers, "ctx": pos + 1,
+                   "kv_cache_GB": round(2 * layers * (pos + 1) * nkv * hd * 2 / 1e9, 2), "parallelism": "none"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel<128,4>", "us_per_launch": per_layer_us,
+                     "bytes_per_launch": head["bytes_per_layer"]},
+        "cpu_baseline": cpu,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

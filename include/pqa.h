@@ -68,8 +68,10 @@ int pqa_set_qk_norm(pqa_ctx* ctx, int layer, const float* q_norm_w, const float*
  * ties-away-from-zero rounding, cpp/quant.hpp:102-135) and written at row pos,
  * then attention of every query head over rows 0..pos.
  * q [n_heads*head_dim], k/v [n_kv_heads*head_dim], out [n_heads*head_dim]:
- * fp32 DEVICE pointers. q/k/v are not modified (the reference normalises
- * in place; the caller never reads them afterwards).
+ * fp32 DEVICE pointers, 16-byte aligned, ready when the context stream
+ * reaches the call (produce them on that stream or synchronise first).
+ * q/k/v are not modified (the reference normalises in place; the caller
+ * never reads them afterwards).
  */
 int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
                float* out);
@@ -80,6 +82,7 @@ int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
  * pointers q [n_tok][n_heads*hd], k/v [n_tok][n_kv*hd], out [n_tok][n_heads*hd].
  * Rows are appended first and attention is causal (token i reads rows
  * 0..start_pos+i), which is what the reference's serial loop computes.
+ * Same alignment and readiness rules as pqa_decode.
  */
 int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q, const float* k,
                 const float* v, float* out);

@@ -33,7 +33,7 @@ static void free_ctx(pqa_ctx* c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm,
-                    c->part_acc,  c->part_ml,   c->counters, c->q16,      c->stage};
+                    c->part_acc,  c->part_ml,   c->q16,      c->stage};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -90,7 +90,7 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     const size_t cache = (size_t)n_layers * c->layer_elems;
     const size_t half = (size_t)head_dim / 2;
     const int ny = n_kv_heads * c->n_chunk;
-    c->max_splits = 256;
+    c->max_splits = 256;  // the split merge holds one (max, weight) per split in LDS
     if (chk(dev_alloc(&c->key_cache, cache), "key cache") && chk(dev_alloc(&c->val_cache, cache), "value cache")) {
         chk(hipMemset(c->key_cache, 0, cache * 2), "memset");
         chk(hipMemset(c->val_cache, 0, cache * 2), "memset");
@@ -103,8 +103,6 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     chk(dev_alloc(&c->qk_norm, (size_t)n_layers * 2 * head_dim), "qk norm");
     chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
     chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
-    if (chk(dev_alloc(&c->counters, (size_t)ny), "counters"))
-        chk(hipMemset(c->counters, 0, (size_t)ny * sizeof(unsigned)), "memset");
     if (rc == PQA_OK) chk(hipDeviceSynchronize(), "sync");
     if (rc != PQA_OK) {
         free_ctx(c);
@@ -118,6 +116,10 @@ extern "C" void pqa_destroy(pqa_ctx* ctx) { free_ctx(ctx); }
 
 extern "C" const char* pqa_last_error(const pqa_ctx* ctx) {
     return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+static bool misaligned(const void* a, const void* b, const void* c, const void* d) {
+    return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d) & 15u) != 0;
 }
 
 static int check_layer(pqa_ctx* ctx, int layer, const char* fn) {
@@ -152,6 +154,7 @@ extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, cons
     if (int rc = check_layer(ctx, layer, "pqa_decode")) return rc;
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: NULL buffer");
+    if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: buffers must be 16-byte aligned");
     return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out), "pqa_decode");
 }
 
@@ -175,6 +178,7 @@ extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, co
     if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill: positions out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: NULL buffer");
+    if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: buffers must be 16-byte aligned");
     if (int rc = ensure_q16(ctx, n_tok)) return rc;
     return hip_check(ctx, pqa::launch_prefill(ctx, layer, start_pos, n_tok, q, k, v, out), "pqa_prefill");
 }

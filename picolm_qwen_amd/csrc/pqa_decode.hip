@@ -14,16 +14,19 @@
 //           v_mfma_f32_16x16x32_f16; q is split into fp16 hi + lo parts
 //           (two MFMAs into one accumulator) so the score keeps fp32
 //           precision; the 1/sqrt(hd) and log2(e) factors are folded into q.
-//   softmax per-head running max over the tile (xor-shuffles across the four
-//           lane groups), exp2, running sum; the accumulator is rescaled
-//           only when a maximum moves.
-//   PV      VALU: each lane holds 8 head dims of one V row (one 16-byte load,
-//           HD/8 lanes per row) and accumulates p[row][h] * v for the G heads;
-//           p reaches the V lanes through a 17x8 float LDS tile per wave.
-// The four waves' (max, sum, acc) are merged in LDS, the workgroup's partial
-// goes to the workspace, and the last workgroup of each (kvh, chunk) to
-// finish (atomic counter) merges all splits with log-sum-exp weights and
-// writes out[h][:] = acc / sum.
+//   softmax each 16-lane group keeps its own running max / sum per head over
+//           the 4 rows of every tile that land in its registers; exp2; the
+//           accumulator is rescaled only when a maximum moves.
+//   PV      VALU (v_fma_mix): the same lane group loads those 4 V rows, each
+//           lane 8 head dims (one 16-byte load, HD/8 lanes per row), and
+//           accumulates p[row][h] * v for the G heads; p comes from lane h of
+//           the group by a DPP row broadcast.
+// Loads run one tile ahead (two register sets, unconditional, row indices
+// clamped to the wave's range) so every wait is for the tile being used.
+// The lane groups are merged once per wave with log-sum-exp weights, the
+// four waves' (max, sum, acc) are merged in LDS, and the workgroup writes
+// either the output (one split) or its partial; decode_combine_kernel then
+// merges the splits of each (kvh, chunk) with log-sum-exp weights.
 #include "pqa_device.h"
 #include "pqa_internal.h"
 
@@ -42,7 +45,6 @@ struct DecodeArgs {
     float* out;
     float* part_acc;
     float* part_ml;
-    unsigned* cnt;
     int pos, g, nchunk, rope, kv_dim, nsplit, rows_per_split;
     float qscale;
 };
@@ -54,23 +56,21 @@ template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
     constexpr int LPR = HD / 8;       // lanes per V row (8 fp16 each)
-    constexpr int RPL = 64 / LPR;     // V rows per wave-wide load
-    constexpr int VL = 16 / RPL;      // V loads per 16-row tile
-    constexpr int PS = 8;             // p-tile row stride (floats)
+    constexpr int VL = 4 * LPR / 16;  // V loads per lane per 16-row tile
     constexpr float NEG_INF = -__builtin_huge_valf();
 
-    __shared__ float sq[G][HD];
-    __shared__ float sk[HD];
-    __shared__ float sv[HD];
+    __shared__ __attribute__((aligned(16))) float sq[G][HD];
+    __shared__ __attribute__((aligned(16))) float sk[HD];
+    __shared__ __attribute__((aligned(16))) float sv[HD];
+    __shared__ __attribute__((aligned(16))) float s_qn[HD];
+    __shared__ __attribute__((aligned(16))) float s_kn[HD];
+    __shared__ __attribute__((aligned(16))) float s_cos[HD / 2];
+    __shared__ __attribute__((aligned(16))) float s_sin[HD / 2];
     __shared__ float s_scale[G + 1];
     __shared__ float s_new[G];
-    __shared__ float sp[4][17 * PS];
     __shared__ float wm[4][G];
     __shared__ float wl[4][G];
     __shared__ float wacc[4][G][HD];
-    __shared__ float sw[kMaxCombineSplits * G];
-    __shared__ float sM[G], sL[G];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -84,14 +84,43 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     const bool owner = split == a.nsplit - 1;
 
     // ---------------- prologue: q heads (and the new K/V row) ----------------
-    for (int i = tid; i < G * HD; i += kDecodeThreads) {
-        const int h = i / HD, d = i - (i / HD) * HD;
-        sq[h][d] = h < Gc ? a.q[(size_t)(h0 + h) * HD + d] : 0.0f;
-    }
-    if (owner) {
-        for (int i = tid; i < HD; i += kDecodeThreads) {
-            sk[i] = a.k[(size_t)kvh * HD + i];
-            sv[i] = a.v[(size_t)kvh * HD + i];
+    // Every global read of the prologue is issued before the first use, as
+    // float4, so the prologue costs one memory round trip.
+    {
+        constexpr int H4 = HD / 4;
+        float4 vq[(G * H4 + kDecodeThreads - 1) / kDecodeThreads];
+#pragma unroll
+        for (int r = 0; r < (G * H4 + kDecodeThreads - 1) / kDecodeThreads; r++) {
+            const int i = tid + r * kDecodeThreads;
+            vq[r] = (i < Gc * H4) ? ((const float4*)(a.q + (size_t)h0 * HD))[i] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        float4 vk = {0.f, 0.f, 0.f, 0.f}, vv = vk, wq = vk, wk = vk, cs = vk;
+        if (owner && tid < H4) {
+            vk = ((const float4*)(a.k + (size_t)kvh * HD))[tid];
+            vv = ((const float4*)(a.v + (size_t)kvh * HD))[tid];
+        }
+        if (a.qn && tid < H4) {
+            wq = ((const float4*)a.qn)[tid];
+            wk = ((const float4*)a.kn)[tid];
+        }
+        // cos row in threads [0, HD/8), sin row in [HD/8, HD/4)
+        if (tid < H4) cs = tid < H4 / 2 ? ((const float4*)a.cosr)[tid] : ((const float4*)a.sinr)[tid - H4 / 2];
+#pragma unroll
+        for (int r = 0; r < (G * H4 + kDecodeThreads - 1) / kDecodeThreads; r++) {
+            const int i = tid + r * kDecodeThreads;
+            if (i < G * H4) ((float4*)&sq[0][0])[i] = vq[r];
+        }
+        if (owner && tid < H4) {
+            ((float4*)sk)[tid] = vk;
+            ((float4*)sv)[tid] = vv;
+        }
+        if (a.qn && tid < H4) {
+            ((float4*)s_qn)[tid] = wq;
+            ((float4*)s_kn)[tid] = wk;
+        }
+        if (tid < H4) {
+            if (tid < H4 / 2) ((float4*)s_cos)[tid] = cs;
+            else ((float4*)s_sin)[tid - H4 / 2] = cs;
         }
     }
     __syncthreads();
@@ -105,10 +134,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     if (a.qn)
         for (int i = tid; i < Gc * HD; i += kDecodeThreads) {
             const int h = i / HD, d = i - (i / HD) * HD;
-            sq[h][d] = rms_apply(sq[h][d], s_scale[h], a.qn[d]);
+            sq[h][d] = rms_apply(sq[h][d], s_scale[h], s_qn[d]);
         }
     if (owner && a.kn)
-        for (int i = tid; i < HD; i += kDecodeThreads) sk[i] = rms_apply(sk[i], s_scale[G], a.kn[i]);
+        for (int i = tid; i < HD; i += kDecodeThreads) sk[i] = rms_apply(sk[i], s_scale[G], s_kn[i]);
     __syncthreads();
     {
         constexpr int HALF = HD / 2;
@@ -118,7 +147,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             float* x = h < Gc ? sq[h] : sk;
             int e0, e1;
             rope_pair(a.rope, p, HD, e0, e1);
-            rope_rotate(x[e0], x[e1], a.cosr[p], a.sinr[p]);
+            rope_rotate(x[e0], x[e1], s_cos[p], s_sin[p]);
         }
     }
     __syncthreads();
@@ -147,8 +176,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     }
 
     // ---------------- wave loop over history rows ----------------
-    const int n = lane & 15;   // MFMA row / column index
-    const int grp = lane >> 4;  // MFMA k-group / output row group
+    // Lane (g, n), g = lane/16, n = lane%16. The score MFMA reads K row n of the
+    // tile and puts S[row 4g+i][head n] in register i of lane (g, n). The same
+    // lane group g also loads V rows 4g..4g+3 (HD/8 lanes per row), so each
+    // group runs its own online softmax over its rows: no cross-group traffic
+    // per tile. p[row][h] reaches the V lanes of the group by a DPP row
+    // broadcast from lane h. The four groups are merged once, at the end.
+    const int n = lane & 15;
+    const int grp = lane >> 4;
     half8 qh[KS], ql[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
@@ -167,6 +202,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     const int w0 = r0 + w * per_w;
     const int w1 = min(rend, w0 + per_w);
 
+    constexpr int RPG = 16 / LPR;  // V rows per lane group per load (1 for HD 128, 2 for HD 64)
+    const int vsub = n / LPR;      // which of those rows this lane takes
+    const int vdim = 8 * (n % LPR);
+
     float m_run = NEG_INF;
     float l_run = 0.0f;
     float acc[G][8];
@@ -175,16 +214,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
 
-    float* p_tile = sp[w];
-    const int vrow = lane / LPR;
-    const int vdim = 8 * (lane % LPR);
-
     if (w0 < w1) {
         const uint16_t* kbase = a.kc + (size_t)kvh * HD + 8 * grp;
         const uint16_t* vbase = a.vc + (size_t)kvh * HD + vdim;
         const size_t stride = (size_t)a.kv_dim;
         const int rlast = w1 - 1;
 
+        // Rows past the wave's range are clamped to its last row: the loads
+        // stay in bounds and hit lines fetched a moment earlier.
         auto load_tile = [&](int tb, u32x4 (&kf)[KS], u32x4 (&vf)[VL]) {
             const int kr = min(tb + n, rlast);
             const uint16_t* kp = kbase + (size_t)kr * stride;
@@ -192,7 +229,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             for (int ks = 0; ks < KS; ks++) kf[ks] = *(const u32x4*)(kp + 32 * ks);
 #pragma unroll
             for (int j = 0; j < VL; j++) {
-                const int vr = min(tb + vrow + RPL * j, rlast);
+                const int vr = min(tb + 4 * grp + vsub + RPG * j, rlast);
                 vf[j] = *(const u32x4*)(vbase + (size_t)vr * stride);
             }
         };
@@ -205,49 +242,40 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
                 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[ks], S, 0, 0, 0);
                 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[ks], S, 0, 0, 0);
             }
-            // lane holds rows tb + 4*grp + i (i = 0..3) of head column n
             float s[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) s[i] = (tb + 4 * grp + i < w1 && n < Gc) ? S[i] : NEG_INF;
-            float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
             const float m_new = fmaxf(m_run, mx);
             const bool moved = m_new > m_run;
-            const bool any_moved = __any(moved);
-            if (any_moved) {
+            if (__any(moved)) {
                 const float corr = moved ? fast_exp2(m_run - m_new) : 1.0f;
                 l_run *= corr;
-                if (grp == 0 && n < PS) p_tile[16 * PS + n] = corr;
                 m_run = m_new;
+#pragma unroll
+                for (int h = 0; h < G; h++) {
+                    const float c = row_bcast(corr, h);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[h][e] *= c;
+                }
             }
-            float psum = 0.0f;
+            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float p = (n < Gc) ? fast_exp2(s[i] - m_run) : 0.0f;
-                psum += p;
-                if (n < PS) p_tile[(4 * grp + i) * PS + n] = p;
-            }
-            l_run += psum;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (any_moved) {
-                float c[G];
-#pragma unroll
-                for (int h = 0; h < G; h++) c[h] = p_tile[16 * PS + h];
-#pragma unroll
-                for (int h = 0; h < G; h++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[h][e] *= c[h];
-            }
+            for (int i = 0; i < 4; i++) p[i] = s[i] == NEG_INF ? 0.0f : fast_exp2(s[i] - m_run);
+            l_run += (p[0] + p[1]) + (p[2] + p[3]);
 #pragma unroll
             for (int j = 0; j < VL; j++) {
-                const int r = vrow + RPL * j;
+                const half8 vh = __builtin_bit_cast(half8, vf[j]);
                 float pr[G];
 #pragma unroll
-                for (int h = 0; h < G; h++) pr[h] = p_tile[r * PS + h];
-                const half8 vh = __builtin_bit_cast(half8, vf[j]);
+                for (int h = 0; h < G; h++) {
+                    if constexpr (RPG == 1) {
+                        pr[h] = row_bcast(p[j], h);
+                    } else {
+                        const float lo = row_bcast(p[RPG * j], h), hi = row_bcast(p[RPG * j + 1], h);
+                        pr[h] = vsub ? hi : lo;
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const float ve = (float)vh[e];
@@ -255,44 +283,49 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
                     for (int h = 0; h < G; h++) acc[h][e] = fmaf(pr[h], ve, acc[h][e]);
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         };
 
         u32x4 kA[KS], vA[VL], kB[KS], vB[VL];
         load_tile(w0, kA, vA);
+        load_tile(w0 + 16, kB, vB);
         for (int tb = w0; tb < w1; tb += 32) {
-            const bool has_b = tb + 16 < w1;
-            if (has_b) load_tile(tb + 16, kB, vB);
             process(tb, kA, vA);
-            if (!has_b) break;
-            if (tb + 32 < w1) load_tile(tb + 32, kA, vA);
+            load_tile(tb + 32, kA, vA);
+            if (tb + 16 >= w1) break;
             process(tb + 16, kB, vB);
+            load_tile(tb + 48, kB, vB);
         }
     }
 
-    // ---------------- merge the wave's lane partials ----------------
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    // ---------------- merge the four lane groups, then write the wave partial ----------------
+    {
+        float M = fmaxf(m_run, __shfl_xor(m_run, 16));
+        M = fmaxf(M, __shfl_xor(M, 32));
+        const float e = (m_run == NEG_INF) ? 0.0f : fast_exp2(m_run - M);
+        float l = l_run * e;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
 #pragma unroll
-    for (int h = 0; h < G; h++)
+        for (int h = 0; h < G; h++) {
+            const float eh = row_bcast(e, h);
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float x = acc[h][e];
+            for (int k = 0; k < 8; k++) {
+                float x = acc[h][k] * eh;
 #pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off);
-            acc[h][e] = x;
+                for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off);
+                acc[h][k] = x;
+            }
         }
-    if (lane < LPR) {
+        if (lane < LPR) {
 #pragma unroll
-        for (int h = 0; h < G; h++)
+            for (int h = 0; h < G; h++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) wacc[w][h][vdim + e] = acc[h][e];
-    }
-    if (lane < G) {
-        wm[w][lane] = m_run;
-        wl[w][lane] = l_run;
+                for (int k = 0; k < 8; k++) wacc[w][h][vdim + k] = acc[h][k];
+        }
+        if (lane < G) {
+            wm[w][lane] = M;
+            wl[w][lane] = l;
+        }
     }
     __syncthreads();
 
@@ -325,47 +358,74 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             }
         }
     }
-    if (a.nsplit == 1) return;
+}
 
-    // ---------------- last workgroup of this (kvh, chunk) merges all splits ----------------
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.cnt[y], 1u);
-        s_last = prev == (unsigned)(a.nsplit - 1);
+// Merge of the split partials of one (KV head, chunk), one workgroup per query
+// head: M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s.
+// A separate launch: the kernel boundary makes every partial visible, so the
+// split workgroups need no fences or atomics.
+template <int HD>
+__global__ __launch_bounds__(kDecodeThreads) void decode_combine_kernel(const float* __restrict__ part_acc,
+                                                                        const float* __restrict__ part_ml,
+                                                                        float* __restrict__ out, int G, int g,
+                                                                        int nchunk, int nsplit) {
+    constexpr int H4 = HD / 4;
+    constexpr int P = kDecodeThreads / H4;  // split groups summed in parallel
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    __shared__ float s_m[kMaxCombineSplits];
+    __shared__ float s_w[kMaxCombineSplits];
+    __shared__ float s_red[kDecodeThreads / 64];
+    __shared__ __attribute__((aligned(16))) floatx4 s_acc[P][H4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x, y = blockIdx.y;
+    const int kvh = y / nchunk, hc = y - kvh * nchunk;
+    const int Gc = min(G, g - hc * G);
+    if (h >= Gc) return;
+    const float* pml = part_ml + ((size_t)y * nsplit * G + h) * 2;
+    float mloc = NEG_INF, lloc = 0.0f;
+    if (tid < nsplit) {
+        mloc = pml[(size_t)tid * G * 2];
+        lloc = pml[(size_t)tid * G * 2 + 1];
+        s_m[tid] = mloc;
     }
+    float M = mloc;
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) s_red[w] = M;
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    const float* pml = a.part_ml + (size_t)y * a.nsplit * G * 2;
-    const float* pacc = a.part_acc + (size_t)y * a.nsplit * G * HD;
-    if (tid < Gc) {
-        float M = NEG_INF;
-        for (int s = 0; s < a.nsplit; s++) M = fmaxf(M, __builtin_nontemporal_load(pml + ((size_t)s * G + tid) * 2));
-        sM[tid] = M;
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float wl = 0.0f;
+    if (tid < nsplit) {
+        const float wt = fast_exp2(mloc - M);
+        s_w[tid] = wt;
+        wl = wt * lloc;
     }
+    for (int off = 32; off > 0; off >>= 1) wl += __shfl_xor(wl, off);
     __syncthreads();
-    for (int i = tid; i < a.nsplit * Gc; i += kDecodeThreads) {
-        const int s = i / Gc, h = i - (i / Gc) * Gc;
-        sw[s * G + h] = fast_exp2(__builtin_nontemporal_load(pml + ((size_t)s * G + h) * 2) - sM[h]);
-    }
+    if (lane == 0) s_red[w] = wl;
     __syncthreads();
-    if (tid < Gc) {
-        float L = 0.0f;
-        for (int s = 0; s < a.nsplit; s++)
-            L += sw[s * G + tid] * __builtin_nontemporal_load(pml + ((size_t)s * G + tid) * 2 + 1);
-        sL[tid] = L;
+    const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const int d4 = tid % H4, pg = tid / H4;
+    const floatx4* src = (const floatx4*)(part_acc + ((size_t)y * nsplit * G + h) * HD) + d4;
+    const size_t sstride = (size_t)G * H4;
+    floatx4 A = {0.f, 0.f, 0.f, 0.f};
+    int sp = pg;
+    for (; sp + 7 * P < nsplit; sp += 8 * P) {
+        floatx4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = src[(size_t)(sp + u * P) * sstride];
+#pragma unroll
+        for (int u = 0; u < 8; u++) A += s_w[sp + u * P] * v[u];
     }
+    for (; sp < nsplit; sp += P) A += s_w[sp] * src[(size_t)sp * sstride];
+    s_acc[pg][d4] = A;
     __syncthreads();
-    for (int i = tid; i < Gc * HD; i += kDecodeThreads) {
-        const int h = i / HD, d = i - (i / HD) * HD;
-        float A = 0.0f;
-        for (int s = 0; s < a.nsplit; s++)
-            A += sw[s * G + h] * __builtin_nontemporal_load(pacc + ((size_t)s * G + h) * HD + d);
-        a.out[(size_t)(h0 + h) * HD + d] = A / sL[h];
+    if (tid < H4) {
+        floatx4 r = s_acc[0][tid];
+#pragma unroll
+        for (int q = 1; q < P; q++) r += s_acc[q][tid];
+        const float inv = 1.0f / L;
+        ((floatx4*)(out + (size_t)(kvh * g + hc * G + h) * HD))[tid] = r * inv;
     }
-    if (tid == 0) a.cnt[y] = 0u;
 }
 
 void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit) {
@@ -398,6 +458,10 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStr
 #undef PQA_CASE
         default: return hipErrorInvalidValue;
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, grid.y), dim3(kDecodeThreads), 0, st, a.part_acc,
+                       a.part_ml, a.out, G, a.g, a.nchunk, a.nsplit);
     return hipGetLastError();
 }
 
@@ -418,7 +482,6 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.out = out;
     a.part_acc = ctx->part_acc;
     a.part_ml = ctx->part_ml;
-    a.cnt = ctx->counters;
     a.pos = pos;
     a.g = ctx->kv_mul;
     a.nchunk = ctx->n_chunk;

@@ -117,4 +117,32 @@ __device__ __forceinline__ float rms_apply(float x, float s, float w) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Value of lane `src` of the caller's 16-lane row (DPP row_newbcast). `src`
+// must fold to a constant after unrolling; the switch then disappears.
+template <int L>
+__device__ __forceinline__ float row_bcast_c(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + L, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row_bcast(float x, int src) {
+    switch (src & 15) {
+        case 0: return row_bcast_c<0>(x);
+        case 1: return row_bcast_c<1>(x);
+        case 2: return row_bcast_c<2>(x);
+        case 3: return row_bcast_c<3>(x);
+        case 4: return row_bcast_c<4>(x);
+        case 5: return row_bcast_c<5>(x);
+        case 6: return row_bcast_c<6>(x);
+        case 7: return row_bcast_c<7>(x);
+        case 8: return row_bcast_c<8>(x);
+        case 9: return row_bcast_c<9>(x);
+        case 10: return row_bcast_c<10>(x);
+        case 11: return row_bcast_c<11>(x);
+        case 12: return row_bcast_c<12>(x);
+        case 13: return row_bcast_c<13>(x);
+        case 14: return row_bcast_c<14>(x);
+        default: return row_bcast_c<15>(x);
+    }
+}
+
 }  // namespace pqa

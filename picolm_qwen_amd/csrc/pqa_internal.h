@@ -25,7 +25,6 @@ struct pqa_ctx {
     // decode split-K workspace
     float* part_acc = nullptr;      // [n_kv*n_chunk][max_splits][chunk_heads][head_dim]
     float* part_ml = nullptr;       // [n_kv*n_chunk][max_splits][chunk_heads][2]
-    unsigned* counters = nullptr;   // [n_kv*n_chunk], zero between calls
     int max_splits = 0;
     int split_override = 0;
     int cu_count = 256;

@@ -42,53 +42,98 @@ constexpr int kPrepThreads = 256;
 
 template <int HD>
 __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(const PrepArgs a) {
-    extern __shared__ float sx[];  // [(nh + nkv) * HD] then [nh + nkv] scales
+    // [(nh + nkv) * HD] q and k heads, then [nh + nkv] scales, [HD] q/k norm
+    // weights, [HD/2] cos and sin of the token's position
+    extern __shared__ __attribute__((aligned(16))) float sx[];
+    constexpr int H4 = HD / 4;
+    constexpr int HALF = HD / 2;
+    constexpr int MAXR = 8;  // float4 loads in flight per thread
     const int tid = threadIdx.x;
     const int tok = blockIdx.x;
     const int pos = a.start + tok;
     const int nheads = a.nh + a.nkv;
     const size_t q_dim = (size_t)a.nh * HD, kv_dim = (size_t)a.nkv * HD;
     float* scale = sx + (size_t)nheads * HD;
+    float* s_qn = scale + ((nheads + 3) & ~3);
+    float* s_kn = s_qn + HD;
+    float* s_cs = s_kn + HD;  // cos then sin
+    const float4* q4 = (const float4*)(a.q + tok * q_dim);
+    const float4* k4 = (const float4*)(a.k + tok * kv_dim);
+    const int nq4 = (int)(q_dim / 4), n4 = nheads * H4;
 
-    for (int i = tid; i < nheads * HD; i += kPrepThreads)
-        sx[i] = i < (int)q_dim ? a.q[tok * q_dim + i] : a.k[tok * kv_dim + (i - q_dim)];
+    // one round trip: every load of a chunk is issued before any store to LDS
+    for (int base = 0; base < n4; base += MAXR * kPrepThreads) {
+        float4 r[MAXR];
+#pragma unroll
+        for (int u = 0; u < MAXR; u++) {
+            const int i = base + tid + u * kPrepThreads;
+            if (i < n4) r[u] = i < nq4 ? q4[i] : k4[i - nq4];
+        }
+#pragma unroll
+        for (int u = 0; u < MAXR; u++) {
+            const int i = base + tid + u * kPrepThreads;
+            if (i < n4) ((float4*)sx)[i] = r[u];
+        }
+    }
+    if (tid < H4) {
+        float4 c = ((const float4*)(a.cos_tab + (size_t)pos * HALF))[tid < H4 / 2 ? tid : 0];
+        float4 sn = ((const float4*)(a.sin_tab + (size_t)pos * HALF))[tid < H4 / 2 ? 0 : tid - H4 / 2];
+        float4 wq = {0.f, 0.f, 0.f, 0.f}, wk = wq;
+        if (a.qn) {
+            wq = ((const float4*)a.qn)[tid];
+            wk = ((const float4*)a.kn)[tid];
+        }
+        ((float4*)s_cs)[tid] = tid < H4 / 2 ? c : sn;
+        ((float4*)s_qn)[tid] = wq;
+        ((float4*)s_kn)[tid] = wk;
+    }
     __syncthreads();
     if (a.qn) {
-        for (int base = 0; base < nheads; base += kPrepThreads / 4) {
-            const int hh = base + (tid >> 2);
+        for (int hb = 0; hb < nheads; hb += kPrepThreads / 4) {
+            const int hh = hb + (tid >> 2);
             if (hh < nheads) scale[hh] = rms_scale_ref_quad(sx + (size_t)hh * HD, HD, tid & 3);
         }
         __syncthreads();
         for (int i = tid; i < nheads * HD; i += kPrepThreads) {
             const int hh = i / HD, d = i - (i / HD) * HD;
-            sx[i] = rms_apply(sx[i], scale[hh], hh < a.nh ? a.qn[d] : a.kn[d]);
+            sx[i] = rms_apply(sx[i], scale[hh], hh < a.nh ? s_qn[d] : s_kn[d]);
         }
         __syncthreads();
     }
-    constexpr int HALF = HD / 2;
-    const float* c = a.cos_tab + (size_t)pos * HALF;
-    const float* s = a.sin_tab + (size_t)pos * HALF;
     for (int i = tid; i < nheads * HALF; i += kPrepThreads) {
         const int hh = i / HALF, p = i - (i / HALF) * HALF;
         int e0, e1;
         rope_pair(a.rope, p, HD, e0, e1);
         float* x = sx + (size_t)hh * HD;
-        rope_rotate(x[e0], x[e1], c[p], s[p]);
+        rope_rotate(x[e0], x[e1], s_cs[p], s_cs[HALF + p]);
     }
     __syncthreads();
-    uint16_t* krow = a.kc + (size_t)pos * kv_dim;
-    uint16_t* vrow = a.vc + (size_t)pos * kv_dim;
-    for (int i = tid; i < (int)kv_dim; i += kPrepThreads) {
-        krow[i] = f32_to_f16_ref(sx[q_dim + i]);
-        vrow[i] = f32_to_f16_ref(a.v[tok * kv_dim + i]);
+    // K and V rows in the reference fp16 rounding, four elements per thread-step
+    const int nkv4 = (int)(kv_dim / 4);
+    const float4* v4 = (const float4*)(a.v + tok * kv_dim);
+    uint2* krow = (uint2*)(a.kc + (size_t)pos * kv_dim);
+    uint2* vrow = (uint2*)(a.vc + (size_t)pos * kv_dim);
+    for (int i = tid; i < nkv4; i += kPrepThreads) {
+        const float4 vv = v4[i];
+        const float4 kk = ((const float4*)(sx + q_dim))[i];
+        krow[i] = uint2{(uint32_t)f32_to_f16_ref(kk.x) | ((uint32_t)f32_to_f16_ref(kk.y) << 16),
+                        (uint32_t)f32_to_f16_ref(kk.z) | ((uint32_t)f32_to_f16_ref(kk.w) << 16)};
+        vrow[i] = uint2{(uint32_t)f32_to_f16_ref(vv.x) | ((uint32_t)f32_to_f16_ref(vv.y) << 16),
+                        (uint32_t)f32_to_f16_ref(vv.z) | ((uint32_t)f32_to_f16_ref(vv.w) << 16)};
     }
     _Float16* qrow = a.q16 + tok * q_dim;
     _Float16* qlo = a.q16_lo ? a.q16_lo + tok * q_dim : nullptr;
-    for (int i = tid; i < (int)q_dim; i += kPrepThreads) {
-        const float x = sx[i] * a.qscale;
-        const _Float16 hi = (_Float16)x;
-        qrow[i] = hi;
-        if (qlo) qlo[i] = (_Float16)(x - (float)hi);
+    for (int i = tid; i < nq4; i += kPrepThreads) {
+        const float4 x4 = ((const float4*)sx)[i];
+        const float xs[4] = {x4.x * a.qscale, x4.y * a.qscale, x4.z * a.qscale, x4.w * a.qscale};
+        half4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            hi[e] = (_Float16)xs[e];
+            lo[e] = (_Float16)(xs[e] - (float)hi[e]);
+        }
+        ((half4*)qrow)[i] = hi;
+        if (qlo) ((half4*)qlo)[i] = lo;
     }
 }
 
@@ -313,7 +358,8 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     p.nkv = ctx->n_kv_heads;
     p.rope = ctx->rope_style;
     p.qscale = 1.4426950408889634f / sqrtf((float)HD);
-    const size_t shm = ((size_t)(ctx->n_heads + ctx->n_kv_heads) * (HD + 1)) * sizeof(float);
+    const int nheads = ctx->n_heads + ctx->n_kv_heads;
+    const size_t shm = ((size_t)nheads * HD + ((nheads + 3) & ~3) + 2 * HD + HD) * sizeof(float);
     hipLaunchKernelGGL(prefill_prep_kernel<HD>, dim3(n_tok), dim3(kPrepThreads), shm, ctx->stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
