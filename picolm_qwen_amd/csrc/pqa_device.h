@@ -117,6 +117,17 @@ __device__ __forceinline__ float rms_apply(float x, float s, float w) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Materialises a loaded value in registers at this point. Placed after a batch
+// of loads whose results are only stored under a predicate, it stops the
+// compiler from sinking each load into its predicated block (which would turn
+// one memory round trip per batch into one per load).
+__device__ __forceinline__ void pin(floatx4& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(float4& x) {
+    floatx4 v = {x.x, x.y, x.z, x.w};
+    asm volatile("" : "+v"(v));
+    x = float4{v[0], v[1], v[2], v[3]};
+}
+
 // Value of lane `src` of the caller's 16-lane row (DPP row_newbcast). `src`
 // must fold to a constant after unrolling; the switch then disappears.
 template <int L>

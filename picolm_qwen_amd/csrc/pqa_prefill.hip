@@ -28,6 +28,7 @@ struct PrepArgs {
     const float* v;
     const float* qn;
     const float* kn;
+    const float* wpad;     // 2*HD readable floats, loaded in place of absent norm weights
     const float* cos_tab;  // [S][HD/2]
     const float* sin_tab;
     uint16_t* kc;
@@ -61,31 +62,42 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(const PrepAr
     const float4* k4 = (const float4*)(a.k + tok * kv_dim);
     const int nq4 = (int)(q_dim / 4), n4 = nheads * H4;
 
-    // one round trip: every load of a chunk is issued before any store to LDS
+    // one round trip: every load of a chunk is issued before any store to LDS;
+    // the loads are unconditional (index clamped) so none sits behind a branch
     for (int base = 0; base < n4; base += MAXR * kPrepThreads) {
         float4 r[MAXR];
 #pragma unroll
         for (int u = 0; u < MAXR; u++) {
-            const int i = base + tid + u * kPrepThreads;
-            if (i < n4) r[u] = i < nq4 ? q4[i] : k4[i - nq4];
+            const int i = min(base + tid + u * kPrepThreads, n4 - 1);
+            const float4* src = i < nq4 ? q4 + i : k4 + (i - nq4);
+            r[u] = *src;
         }
+#pragma unroll
+        for (int u = 0; u < MAXR; u++) pin(r[u]);
 #pragma unroll
         for (int u = 0; u < MAXR; u++) {
             const int i = base + tid + u * kPrepThreads;
             if (i < n4) ((float4*)sx)[i] = r[u];
         }
     }
-    if (tid < H4) {
-        float4 c = ((const float4*)(a.cos_tab + (size_t)pos * HALF))[tid < H4 / 2 ? tid : 0];
-        float4 sn = ((const float4*)(a.sin_tab + (size_t)pos * HALF))[tid < H4 / 2 ? 0 : tid - H4 / 2];
-        float4 wq = {0.f, 0.f, 0.f, 0.f}, wk = wq;
-        if (a.qn) {
-            wq = ((const float4*)a.qn)[tid];
-            wk = ((const float4*)a.kn)[tid];
+    {
+        const int t = tid % H4;  // every thread loads (in bounds); the first H4 store
+        const float4* cs = t < H4 / 2 ? (const float4*)(a.cos_tab + (size_t)pos * HALF) + t
+                                      : (const float4*)(a.sin_tab + (size_t)pos * HALF) + (t - H4 / 2);
+        const float4 c = *cs;
+        const float* qn = a.qn ? a.qn : a.wpad;  // loads stay unconditional without a norm
+        const float* kn = a.kn ? a.kn : a.wpad + HD;
+        const float4 wq = ((const float4*)qn)[t];
+        float4 wk = ((const float4*)kn)[t];
+        float4 c2 = c, wq2 = wq;
+        pin(c2);
+        pin(wq2);
+        pin(wk);
+        if (tid < H4) {
+            ((float4*)s_cs)[tid] = c2;
+            ((float4*)s_qn)[tid] = wq2;
+            ((float4*)s_kn)[tid] = wk;
         }
-        ((float4*)s_cs)[tid] = tid < H4 / 2 ? c : sn;
-        ((float4*)s_qn)[tid] = wq;
-        ((float4*)s_kn)[tid] = wk;
     }
     __syncthreads();
     if (a.qn) {
@@ -346,6 +358,7 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     const bool norm = ctx->has_qk_norm[layer] != 0;
     p.qn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD : nullptr;
     p.kn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD + HD : nullptr;
+    p.wpad = ctx->qk_norm;
     p.cos_tab = ctx->rope_cos;
     p.sin_tab = ctx->rope_sin;
     p.kc = ctx->key_cache + (size_t)layer * ctx->layer_elems;

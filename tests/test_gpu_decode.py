@@ -78,6 +78,14 @@ def test_decode_split_sizes(split):
     _decode_case(50, 16, 8, 128, 2048, 0, 1e6, True, 2000, 0.0, split=split)
 
 
+def test_last_table_row_without_qk_norm():
+    # Regression: with no QK-norm the kernel once loaded its placeholder norm
+    # weights from the RoPE row at pos, reading past the end of the table when
+    # pos == max_seq_len - 1 and the table ends on an allocation boundary.
+    print("decode last row, no qk-norm, 131072-entry table", flush=True)
+    _decode_case(60, 16, 8, 128, 131072, 0, 1e6, False, 131071, 0.0)
+
+
 def test_pos_ctx1_is_v_exactly():
     # ctx = 1: softmax of one row is 1, so out = fp16(v) exactly (cpp/model.hpp:387-413)
     nh, nkv, hd, smax = 8, 2, 128, 16

@@ -63,6 +63,13 @@ def test_prefill_matches_oracle(case):
     _prefill_case(CASES.index(case), *case[1:])
 
 
+def test_prefill_to_last_table_row_without_qk_norm():
+    # Same regression as the decode test: the prompt ends on the last row of
+    # a table that ends on an allocation boundary, no QK-norm.
+    print("prefill to last row, no qk-norm", flush=True)
+    _prefill_case(41, 16, 8, 128, 65536, 0, 1e6, False, 65536 - 300, 300, 0.0)
+
+
 def test_prefill_split_q_mode_on_plain_inputs():
     print("prefill split-q mode", flush=True)
     _prefill_case(40, 32, 8, 128, 300, 0, 1e6, True, 20, 250, 0.0, split_q=True)
