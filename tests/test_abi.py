@@ -1,0 +1,76 @@
+"""The C ABI without a GPU: libpqa.so loads, exports every function declared in
+include/pqa.h, validates arguments before touching the device, reports errors
+through pqa_last_error, and its host-side RoPE table equals the reference's."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+from picolm_qwen_amd import _lib
+from picolm_qwen_amd._build import LIB
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "pqa.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pqa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built_in_tree():
+    assert os.path.exists(LIB), "run __graft_entry__.build()"
+
+
+def test_exports_every_declared_function():
+    L = C.CDLL(LIB)
+    names = header_functions()
+    assert len(names) >= 18
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert sorted(_lib.EXPORTS) == names
+
+
+def test_create_rejects_bad_shapes_before_any_device_call():
+    L = _lib.lib()
+    h = C.c_void_p()
+    tab = np.zeros(64 * 48, np.float32)
+    p = tab.ctypes.data_as(C.c_void_p)
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 96, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
+    assert b"head_dim" in L.pqa_last_error(None)
+    assert L.pqa_create(C.byref(h), 1, 64, 6, 4, 64, 0, p, p) == _lib.PQA_ERR_ARG
+    assert b"multiple" in L.pqa_last_error(None)
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 64, 3, p, p) == _lib.PQA_ERR_ARG
+    assert L.pqa_create(C.byref(h), 0, 64, 8, 2, 64, 0, p, p) == _lib.PQA_ERR_ARG
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 64, 0, None, None) == _lib.PQA_ERR_ARG
+    assert L.pqa_create(None, 1, 64, 8, 2, 64, 0, p, p) == _lib.PQA_ERR_ARG
+
+
+def test_null_context_calls_fail_cleanly():
+    L = _lib.lib()
+    assert L.pqa_decode(None, 0, 0, None, None, None, None) == _lib.PQA_ERR_ARG
+    assert L.pqa_prefill(None, 0, 0, 1, None, None, None, None) == _lib.PQA_ERR_ARG
+    assert L.pqa_sync(None) == _lib.PQA_ERR_ARG
+    assert L.pqa_stream(None) is None
+    L.pqa_destroy(None)
+
+
+@pytest.mark.parametrize("base,hd", [(1e4, 64), (1e6, 128)])
+def test_host_rope_table_equals_oracle_and_reference_formula(base, hd):
+    from picolm_qwen_amd import rope_table
+    c, s = rope_table(base, hd, 300)
+    oc, os_ = O.rope_table(base, hd, 300)
+    assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+
+
+def test_python_wrapper_raises_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from picolm_qwen_amd import PicoAttention, PQAError
+    with pytest.raises(PQAError):
+        PicoAttention(1, 64, 8, 2, 64)
