@@ -15,6 +15,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short short4v __attribute__((ext_vector_type(4)));
 
 // fp32 -> fp16 exactly as cpp/quant.hpp:102-135 rounds: the magnitude gets
 // half an fp16 ulp added and is truncated (nearest, ties away from zero).

@@ -155,196 +155,209 @@ struct AttnArgs {
     const uint16_t* kc;
     const uint16_t* vc;
     float* out;
-    int start, n_tok, nh, g, kv_dim, rows, nblk;
+    int start, n_tok, nh, g, n_kv, kv_dim, rows, nblk;
 };
 
 constexpr int kAttnThreads = 256;
 constexpr int kRowsPerBlock = 128;
 constexpr int kKeysPerTile = 64;
 
+// LDS tile layout: 64 rows of HD fp16 (row = one key), rows unpadded, the
+// 16-byte chunks of row r stored at chunk index c ^ swz(r). The direct
+// global->LDS loads pick, for each lane, the global chunk whose swizzled slot
+// is the lane's LDS slot, so the tile is written already swizzled.
+//   K: swz(r) = r mod chunks: the A-operand reads (32 rows, one chunk
+//      column) hit 16 distinct chunk slots per 16 lanes.
+//   V: swz(r) = 4 * (r mod 4): the transposed reads (8 rows x 4 chunks per
+//      instruction) touch every chunk slot exactly twice (the 2-pass minimum).
 template <int HD>
-struct AttnTile {
-    static constexpr int KST = HD + 8;              // K row stride in LDS (halves)
-    static constexpr int VST = kKeysPerTile + 4;    // V^T row stride (halves)
-    static constexpr int KCH = kKeysPerTile * HD / 8 / kAttnThreads;  // 16-B K chunks per thread
-    static constexpr int VCH = KCH;
-    static constexpr int DBLK = HD / 8;             // 16-B chunks per row
+struct PrefillTile {
+    static constexpr int CH = HD / 8;            // 16-byte chunks per row
+    static constexpr int ROWB = HD * 2;          // bytes per row
+    static constexpr int BYTES = kKeysPerTile * ROWB;
+    static constexpr int RPI = 1024 / ROWB;      // rows per 1 KB wave-wide load
+    static constexpr int NI = BYTES / 1024 / (kAttnThreads / 64);  // loads per wave per tile and operand
+    __device__ static int swz_k(int r) { return r & (CH - 1); }
+    __device__ static int swz_v(int r) { return (4 * (r & 3)) & (CH - 1); }
 };
 
 // SPLITQ: scores use q = hi + lo (two fp16 MFMAs into one fp32 accumulator),
 // which keeps fp32-level score precision when keys carry large outliers.
 template <int HD, bool SPLITQ>
 __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const AttnArgs a) {
-    using T = AttnTile<HD>;
-    constexpr int QK = HD / 16;   // k-steps of S^T = K Q^T
-    constexpr int DT = HD / 32;   // 32-dim tiles of O^T
+    using T = PrefillTile<HD>;
+    constexpr int QK = HD / 16;  // k-steps of S^T = K Q^T
+    constexpr int DT = HD / 32;  // 32-dim tiles of O^T
     constexpr float NEG_INF = -__builtin_huge_valf();
-    __shared__ __attribute__((aligned(16))) _Float16 sK[kKeysPerTile * T::KST];
-    __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * T::VST];
+    __shared__ __attribute__((aligned(1024))) char lds[2][2][T::BYTES];  // [buffer][K, V]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
-    const int col = lane & 31;   // q row within the wave / MFMA row index
-    const int hk = lane >> 5;    // MFMA k-group
-    const int kvh = blockIdx.y;
+    const int col = lane & 31;  // q row within the wave / MFMA row index
+    const int hk = lane >> 5;   // MFMA k-group
+    // Work item: all blocks of one KV head run on the same XCD (workgroups go
+    // round-robin over the 8 XCDs), keeping that head's K/V in one L2. Within a
+    // head, the first half of the items are the long causal blocks in
+    // decreasing length, the second half the short ones in increasing length,
+    // so the two workgroups a CU receives add up to about the same work.
+    const int kvh = (int)blockIdx.x % a.n_kv;
+    const int jj = (int)blockIdx.x / a.n_kv;
+    const int half = (a.nblk + 1) / 2;
+    const int b = jj < half ? a.nblk - 1 - jj : jj - half;
+
     const uint16_t* kbase = a.kc + (size_t)kvh * HD;
     const uint16_t* vbase = a.vc + (size_t)kvh * HD;
 
-    const int b_first = a.nblk - 1 - (int)blockIdx.x;
-    const int b_second = (int)blockIdx.x;
-    for (int pass = 0; pass < 2; pass++) {
-        const int b = pass == 0 ? b_first : b_second;
-        if (pass == 1 && b_second >= b_first) break;
+    const int R0 = b * kRowsPerBlock + w * 32;
+    const int R = R0 + col;
+    const bool rvalid = R < a.rows;
+    const int tok = rvalid ? R / a.g : 0;
+    const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
+    const int qpos = a.start + tok;
+    const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
+    const int kend = a.start + last_row_blk / a.g + 1;
+    const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
+    const int kend_w = R0 < a.rows ? a.start + (min(a.rows, R0 + 32) - 1) / a.g + 1 : 0;
+    const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
 
-        const int R0 = b * kRowsPerBlock + w * 32;
-        const int R = R0 + col;
-        const bool rvalid = R < a.rows;
-        const int tok = rvalid ? R / a.g : 0;
-        const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
-        const int qpos = a.start + tok;
-
-        half8 qf[QK], qfl[SPLITQ ? QK : 1];
-        {
-            const size_t qoff = ((size_t)tok * a.nh + hq) * HD + 8 * hk;
+    // direct global -> LDS loads of tile kt into buffer buf (each wave its share)
+    auto issue = [&](int kt, int buf) {
+        const int key0 = kt * kKeysPerTile;
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++) {
-                const u32x4 raw = rvalid ? *(const u32x4*)(a.q16 + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
-                qf[ks] = __builtin_bit_cast(half8, raw);
-                if constexpr (SPLITQ) {
-                    const u32x4 rl = rvalid ? *(const u32x4*)(a.q16_lo + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
-                    qfl[ks] = __builtin_bit_cast(half8, rl);
-                }
+        for (int i = 0; i < T::NI; i++) {
+            const int inst = w * T::NI + i;
+            const int r = inst * T::RPI + lane / T::CH;
+            const int p = lane % T::CH;
+            const size_t row = (size_t)min(key0 + r, kend - 1) * a.kv_dim;
+            const uint16_t* gk = kbase + row + 8 * (p ^ T::swz_k(r));
+            const uint16_t* gv = vbase + row + 8 * (p ^ T::swz_v(r));
+            __builtin_amdgcn_global_load_lds((const void*)gk, (__attribute__((address_space(3))) void*)&lds[buf][0][inst * 1024],
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)gv, (__attribute__((address_space(3))) void*)&lds[buf][1][inst * 1024],
+                                             16, 0, 0);
+        }
+    };
+
+    issue(0, 0);
+
+    half8 qf[QK], qfl[SPLITQ ? QK : 1];
+    {
+        const size_t qoff = ((size_t)tok * a.nh + hq) * HD + 8 * hk;
+#pragma unroll
+        for (int ks = 0; ks < QK; ks++) {
+            const u32x4 raw = rvalid ? *(const u32x4*)(a.q16 + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+            qf[ks] = __builtin_bit_cast(half8, raw);
+            if constexpr (SPLITQ) {
+                const u32x4 rl = rvalid ? *(const u32x4*)(a.q16_lo + qoff + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+                qfl[ks] = __builtin_bit_cast(half8, rl);
             }
         }
-        const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
-        const int kend = a.start + last_row_blk / a.g + 1;
-        const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
-        const int kend_w = R0 < a.rows ? a.start + (min(a.rows, R0 + 32) - 1) / a.g + 1 : 0;
-        const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
+    }
 
-        float m_run = NEG_INF, l_run = 0.0f;
-        floatx16 o[DT];
+    float m_run = NEG_INF, l_run = 0.0f;
+    floatx16 o[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
 
-        // global -> register staging of one K/V tile
-        u32x4 kreg[T::KCH], vreg[T::VCH];
-        auto gload = [&](int key0) {
-#pragma unroll
-            for (int j = 0; j < T::KCH; j++) {
-                const int c = tid + j * kAttnThreads;
-                const int key = min(key0 + c / T::DBLK, kend - 1);
-                kreg[j] = *(const u32x4*)(kbase + (size_t)key * a.kv_dim + 8 * (c % T::DBLK));
-            }
-#pragma unroll
-            for (int j = 0; j < T::VCH; j++) {
-                const int key = min(key0 + (tid & 63), kend - 1);
-                const int dblk = (tid >> 6) + 4 * j;
-                vreg[j] = *(const u32x4*)(vbase + (size_t)key * a.kv_dim + 8 * dblk);
-            }
-        };
-        auto lds_store = [&]() {
-#pragma unroll
-            for (int j = 0; j < T::KCH; j++) {
-                const int c = tid + j * kAttnThreads;
-                *(u32x4*)(sK + (c / T::DBLK) * T::KST + 8 * (c % T::DBLK)) = kreg[j];
-            }
-#pragma unroll
-            for (int j = 0; j < T::VCH; j++) {
-                const int kk = tid & 63;
-                const int dblk = (tid >> 6) + 4 * j;
-                const half8 vv = __builtin_bit_cast(half8, vreg[j]);
-#pragma unroll
-                for (int e = 0; e < 8; e++) sVt[(8 * dblk + e) * T::VST + kk] = vv[e];
-            }
-        };
+    // transposed-read geometry of this lane (see the V layout above)
+    const int j16 = lane & 15, g16 = lane >> 4;
+    const int tr_e = j16 >> 2, tr_q = j16 & 3;
 
-        gload(0);
-        for (int kt = 0; kt < ntiles; kt++) {
-            const int key0 = kt * kKeysPerTile;
-            __syncthreads();  // previous tile's LDS reads are done
-            lds_store();
-            __syncthreads();
-            if (kt + 1 < ntiles) gload(key0 + kKeysPerTile);
-            if (key0 >= kend_w) continue;  // wave-uniform: every row of this wave is done
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int buf = kt & 1;
+        const int key0 = kt * kKeysPerTile;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of tile kt
+        __syncthreads();                                   // everyone's; buffer buf^1 is free
+        if (kt + 1 < ntiles) issue(kt + 1, buf ^ 1);
+        if (key0 >= kend_w) continue;  // wave-uniform: every row of this wave is done
 
-            floatx16 sacc[2];
+        const char* kt_lds = lds[buf][0];
+        const char* vt_lds = lds[buf][1];
+        floatx16 sacc[2];
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) {
+        for (int t2 = 0; t2 < 2; t2++) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) sacc[t2][r] = 0.0f;
-                const _Float16* kp = sK + (32 * t2 + col) * T::KST + 8 * hk;
+            for (int r = 0; r < 16; r++) sacc[t2][r] = 0.0f;
+            const int row = 32 * t2 + col;
 #pragma unroll
-                for (int ks = 0; ks < QK; ks++) {
-                    const half8 kf = *(const half8*)(kp + 16 * ks);
-                    sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sacc[t2], 0, 0, 0);
-                    if constexpr (SPLITQ)
-                        sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfl[ks], sacc[t2], 0, 0, 0);
-                }
+            for (int ks = 0; ks < QK; ks++) {
+                const int c = 2 * ks + hk;
+                const half8 kf = *(const half8*)(kt_lds + row * T::ROWB + 16 * (c ^ T::swz_k(row)));
+                sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sacc[t2], 0, 0, 0);
+                if constexpr (SPLITQ)
+                    sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfl[ks], sacc[t2], 0, 0, 0);
             }
-            // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
-            if (key0 + kKeysPerTile - 1 > qpos_min_w) {
-#pragma unroll
-                for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
-                        if (key > qpos) sacc[t2][r] = NEG_INF;
-                    }
-            }
-            float mx = NEG_INF;
-#pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float corr = fast_exp2(m_run - m_new);
-            m_run = m_new;
-            float psum = 0.0f;
-            half8 pf[4];
+        }
+        // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
+        if (key0 + kKeysPerTile - 1 > qpos_min_w) {
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const float p = fast_exp2(sacc[t2][r] - m_new);
-                    psum += p;
-                    pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)p;
+                    const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
+                    if (key > qpos) sacc[t2][r] = NEG_INF;
                 }
-            l_run = l_run * corr + psum;
+        }
+        float mx = NEG_INF;
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float corr = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.0f;
+        half8 pf[4];
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    const _Float16* vp = sVt + (32 * dt + col) * T::VST + 16 * s + 4 * hk;
-                    const u32x2 lo = *(const u32x2*)vp;
-                    const u32x2 hi = *(const u32x2*)(vp + 8);
-                    const u32x4 raw = {lo[0], lo[1], hi[0], hi[1]};
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, raw), pf[s],
-                                                                   o[dt], 0, 0, 0);
+            for (int r = 0; r < 16; r++) {
+                const float p = fast_exp2(sacc[t2][r] - m_new);
+                psum += p;
+                pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)p;
+            }
+        l_run = l_run * corr + psum;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                half4 part[2];
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const int row = 16 * s + 8 * t + 4 * hk + tr_e;
+                    const int dim = 32 * dt + 16 * (g16 & 1) + 4 * tr_q;
+                    const int c = dim >> 3;
+                    const char* adr = vt_lds + row * T::ROWB + 16 * (c ^ T::swz_v(row)) + 2 * (dim & 7);
+                    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4v*)adr);
+                    part[t] = __builtin_bit_cast(half4, raw);
                 }
+                const half8 vf = {part[0][0], part[0][1], part[0][2], part[0][3],
+                                  part[1][0], part[1][1], part[1][2], part[1][3]};
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[s], o[dt], 0, 0, 0);
             }
         }
-        const float l_tot = l_run + __shfl_xor(l_run, 32);
-        if (rvalid) {
-            const float inv = 1.0f / l_tot;
-            float* op = a.out + ((size_t)tok * a.nh + hq) * HD + 4 * hk;
+    }
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (rvalid) {
+        const float inv = 1.0f / l_tot;
+        float* op = a.out + ((size_t)tok * a.nh + hq) * HD + 4 * hk;
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+        for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    floatx4 vv = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
-                                  o[dt][4 * r4 + 3] * inv};
-                    *(floatx4*)(op + 32 * dt + 8 * r4) = vv;
-                }
-        }
+            for (int r4 = 0; r4 < 4; r4++) {
+                floatx4 vv = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                              o[dt][4 * r4 + 3] * inv};
+                *(floatx4*)(op + 32 * dt + 8 * r4) = vv;
+            }
     }
 }
 
@@ -387,10 +400,11 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     a.n_tok = n_tok;
     a.nh = ctx->n_heads;
     a.g = ctx->kv_mul;
+    a.n_kv = ctx->n_kv_heads;
     a.kv_dim = (int)ctx->kv_dim;
     a.rows = n_tok * ctx->kv_mul;
     a.nblk = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    dim3 grid((a.nblk + 1) / 2, ctx->n_kv_heads);
+    dim3 grid(a.nblk * ctx->n_kv_heads);
     if (splitq) hipLaunchKernelGGL((prefill_attn_kernel<HD, true>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     else hipLaunchKernelGGL((prefill_attn_kernel<HD, false>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     return hipGetLastError();
