@@ -59,37 +59,38 @@ struct DecodeArgs {
 
 constexpr int kDecodeWaves = 8;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
+constexpr int kDecodeTiles = 2;  // 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
+constexpr int kCombineDims = 32;  // head dims per combine workgroup
 constexpr int kMaxCombineSplits = 256;
 
 template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
     constexpr int NW = kDecodeWaves;
+    constexpr int NT = kDecodeTiles;
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
     constexpr int LPR = HD / 8;       // lanes per V row (8 fp16 each)
     constexpr int VL = 4 * LPR / 16;  // V loads per lane per 16-row tile
     constexpr int RPG = 16 / LPR;     // V rows per lane group per load (1 for HD 128, 2 for HD 64)
-    constexpr int H4 = HD / 4;
-    constexpr int HALF = HD / 2;
-    constexpr int QR = (NW * G * H4 + kDecodeThreads - 1) / kDecodeThreads;  // q float4 loads per thread
+    constexpr int H4 = HD / 4;        // float4s per head
+    constexpr int QL = (G * H4 + 63) / 64;  // q float4 loads per lane
+    constexpr int QS = HD + 4;        // padded LDS row stride of a head
     constexpr float NEG_INF = -__builtin_huge_valf();
 
-    // q heads of every column ([NW][G][HD]); after the fragments are built the
-    // same space holds the wave partials ([NW][G][HD]).
-    __shared__ __attribute__((aligned(16))) float sqw[NW * G * HD];
-    __shared__ __attribute__((aligned(16))) float sk[NW][HD];
-    __shared__ __attribute__((aligned(16))) float sv[NW][HD];
-    __shared__ __attribute__((aligned(16))) float s_qn[HD];
-    __shared__ __attribute__((aligned(16))) float s_kn[HD];
-    __shared__ __attribute__((aligned(16))) float s_cs[HD];  // cos row | sin row
-    __shared__ float s_scale[NW * G + NW];
+    // Per wave: its column's q heads ([G][QS], raw, then normalised, rotated
+    // and scaled), later the wave's partial accumulator. Per wave: the K row
+    // for the exact norm and the norm scales. Per column: the new row's V and
+    // scores. Every region but the last three is private to one wave.
+    __shared__ __attribute__((aligned(16))) float sq[NW][G * QS];
+    __shared__ __attribute__((aligned(16))) float skr[NW][HD];
+    __shared__ float s_scale[NW][G + 1];
+    __shared__ __attribute__((aligned(16))) float s_vnew[NW][HD];
     __shared__ float s_new[NW][G];
     __shared__ float wm[NW][G];
     __shared__ float wl[NW][G];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int split = blockIdx.x;
     const int ybase = blockIdx.y * NW;
     const int cols = min(a.ny - ybase, NW);
@@ -98,20 +99,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     const int c = active ? w % cols : 0;
     const int sb = active ? w / cols : 0;
     const bool owner = split == a.nsplit - 1;
+    const bool writer = active && owner && sb == 0;  // this wave adds column c's new row
+    // column c = (KV head, chunk of at most G query heads)
+    const int kvh = (ybase + c) / a.nchunk;
+    const int hc = ybase + c - kvh * a.nchunk;
+    const int Gc = min(G, a.g - hc * G);
+    const int h0 = kvh * a.g + hc * G;
 
-    // first query head, KV head, chunk index and head count of column cc
-    auto col_h0 = [&](int cc, int& kvh_o, int& hc_o, int& gc_o) {
-        const int yy = ybase + cc;
-        kvh_o = yy / a.nchunk;
-        hc_o = yy - kvh_o * a.nchunk;
-        gc_o = min(G, a.g - hc_o * G);
-        return kvh_o * a.g + hc_o * G;
-    };
-    int kvh, hc, Gc;
-    const int h0 = col_h0(c, kvh, hc, Gc);
-    (void)hc;
-
-    // ---------------- this wave's history rows; first two tiles in flight ----------------
+    // ---------------- this wave's history rows; first tiles in flight ----------------
     // The first K/V tiles do not depend on q, so they are requested with the
     // prologue's loads. Loads are unconditional: an empty range (or pos == 0)
     // clamps to row 0, which is allocated and never used.
@@ -140,122 +135,108 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             vf[j] = __builtin_nontemporal_load((const u32x4*)(vbase + (size_t)vr * stride));
         }
     };
-    u32x4 kA[KS], vA[VL], kB[KS], vB[VL];
+    u32x4 kt[NT][KS], vt[NT][VL];
 
-    // ---------------- prologue: q heads of every column, the new K/V rows ----------------
-    {
-        float4 vq[QR];
+    // ---------------- prologue, one wave per column, no workgroup barrier ----------------
+    // Lane layout: float4 i = lane + 64 r of the column's q heads is
+    // (head i / H4, elements 4t..4t+3), t = lane mod H4; the K and V rows of
+    // the KV head use the same t, so q[h][4t..] and k[4t..] share a lane.
+    const int t = lane % H4;
+    float4 vq[QL];
 #pragma unroll
-        for (int r = 0; r < QR; r++) {
-            const int i = min(tid + r * kDecodeThreads, cols * G * H4 - 1);
-            const int cc = i / (G * H4), rem = i - cc * (G * H4), h = rem / H4, d4 = rem - h * H4;
-            int kq, hq, gq;
-            const int hb = col_h0(cc, kq, hq, gq);
-            vq[r] = ((const float4*)(a.q + (size_t)(hb + min(h, gq - 1)) * HD))[d4];
-        }
-        const int t = tid % (NW * H4);
-        int kk_, hk_, gk_;
-        col_h0(min(t / H4, cols - 1), kk_, hk_, gk_);
-        float4 vk = ((const float4*)(a.k + (size_t)kk_ * HD))[t % H4];
-        float4 vv = ((const float4*)(a.v + (size_t)kk_ * HD))[t % H4];
-        const int t4 = tid % H4;
-        const float* qn = a.qn ? a.qn : a.wpad;  // loads stay unconditional without a norm
-        const float* kn = a.kn ? a.kn : a.wpad + HD;
-        float4 wq = ((const float4*)qn)[t4];
-        float4 wk = ((const float4*)kn)[t4];
-        float4 cs = t4 < H4 / 2 ? ((const float4*)a.cosr)[t4] : ((const float4*)a.sinr)[t4 - H4 / 2];
-        load_tile(w0, kA, vA);
-        load_tile(w0 + 16, kB, vB);
+    for (int r = 0; r < QL; r++) {
+        const int hh = min((lane + 64 * r) / H4, Gc - 1);
+        vq[r] = ((const float4*)(a.q + (size_t)(h0 + hh) * HD))[t];
+    }
+    float4 vk = ((const float4*)(a.k + (size_t)kvh * HD))[t];
+    float4 vv = ((const float4*)(a.v + (size_t)kvh * HD))[t];
+    const float* qn = a.qn ? a.qn : a.wpad;  // loads stay unconditional without a norm
+    const float* kn = a.kn ? a.kn : a.wpad + HD;
+    float4 wq = ((const float4*)qn)[t];
+    float4 wk = ((const float4*)kn)[t];
+    const int ci = rope_angle_f4<HD>(a.rope, t);
+    float4 cs = ((const float4*)a.cosr)[ci];
+    float4 sn = ((const float4*)a.sinr)[ci];
 #pragma unroll
-        for (int r = 0; r < QR; r++) pin(vq[r]);
-        pin(vk);
-        pin(vv);
-        pin(wq);
-        pin(wk);
-        pin(cs);
+    for (int b = 0; b < NT; b++) load_tile(w0 + 16 * b, kt[b], vt[b]);
 #pragma unroll
-        for (int r = 0; r < QR; r++) {
-            const int i = tid + r * kDecodeThreads;
-            if (i < NW * G * H4) {
-                const int cc = i / (G * H4), h = (i - cc * (G * H4)) / H4;
-                int kq, hq, gq;
-                col_h0(min(cc, cols - 1), kq, hq, gq);
-                ((float4*)sqw)[i] = (cc < cols && h < gq) ? vq[r] : float4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < QL; r++) pin(vq[r]);
+    pin(vk);
+    pin(vv);
+    pin(wq);
+    pin(wk);
+    pin(cs);
+    pin(sn);
+
+    float* q_lds = sq[w];
+    if (active) {
+        // QK-RMSNorm scales in the reference's summation order: quad j of lane
+        // 4h+j sums x[j], x[j+4], ... sequentially (heads h < Gc, then the K row).
+        if (a.qn) {
+#pragma unroll
+            for (int r = 0; r < QL; r++) {
+                const int i = lane + 64 * r;
+                if (i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
+            }
+            if (writer && lane < H4) ((float4*)skr[w])[t] = vk;
+            wave_sync();
+            const int qd = lane >> 2;
+            const bool is_k = qd == Gc;
+            const float* src = is_k ? skr[w] : q_lds + min(qd, Gc - 1) * QS;
+            const float s = rms_scale_ref_quad(src, HD, lane & 3);
+            if ((lane & 3) == 0 && (qd < Gc || (is_k && writer))) s_scale[w][qd] = s;
+            wave_sync();
+#pragma unroll
+            for (int r = 0; r < QL; r++) {
+                const float sc = s_scale[w][min((lane + 64 * r) / H4, Gc - 1)];
+                vq[r] = float4{rms_apply(vq[r].x, sc, wq.x), rms_apply(vq[r].y, sc, wq.y),
+                               rms_apply(vq[r].z, sc, wq.z), rms_apply(vq[r].w, sc, wq.w)};
+            }
+            if (writer) {
+                const float sc = s_scale[w][Gc];
+                vk = float4{rms_apply(vk.x, sc, wk.x), rms_apply(vk.y, sc, wk.y), rms_apply(vk.z, sc, wk.z),
+                            rms_apply(vk.w, sc, wk.w)};
             }
         }
-        if (tid < NW * H4) {
-            ((float4*)&sk[0][0])[tid] = vk;
-            ((float4*)&sv[0][0])[tid] = vv;
+#pragma unroll
+        for (int r = 0; r < QL; r++) {
+            vq[r] = rope_lanes<HD>(vq[r], a.rope, t, cs, sn);
+            vq[r] = float4{vq[r].x * a.qscale, vq[r].y * a.qscale, vq[r].z * a.qscale, vq[r].w * a.qscale};
         }
-        if (tid < H4) {
-            ((float4*)s_qn)[tid] = wq;
-            ((float4*)s_kn)[tid] = wk;
-            ((float4*)s_cs)[tid] = cs;
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < QL; r++) {
+            const int i = lane + 64 * r;
+            if (i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
         }
-    }
-    __syncthreads();
-    {
-        // QK-RMSNorm scales, one quad per head: q heads [0, NW*G), K rows after.
-        const int qd = tid >> 2, j = tid & 3;
-        if (a.qn && qd < cols * G) {
-            int kq, hq, gq;
-            col_h0(qd / G, kq, hq, gq);
-            if (qd % G < gq) s_scale[qd] = rms_scale_ref_quad(sqw + (size_t)qd * HD, HD, j);
-        } else if (a.kn && owner && qd >= NW * G && qd < NW * G + cols) {
-            s_scale[qd] = rms_scale_ref_quad(sk[qd - NW * G], HD, j);
-        }
-    }
-    __syncthreads();
-    if (a.qn) {
-        for (int i = tid; i < cols * G * HD; i += kDecodeThreads) {
-            const int hh = i / HD, d = i - hh * HD;
-            int kq, hq, gq;
-            col_h0(hh / G, kq, hq, gq);
-            if (hh % G < gq) sqw[i] = rms_apply(sqw[i], s_scale[hh], s_qn[d]);
-        }
-        if (owner)
-            for (int i = tid; i < cols * HD; i += kDecodeThreads) {
-                const int cc = i / HD, d = i - cc * HD;
-                sk[cc][d] = rms_apply(sk[cc][d], s_scale[NW * G + cc], s_kn[d]);
+        if (writer) {
+            // new K/V row: rotate, round to fp16 as the reference does, store
+            // once per KV head (chunk 0), keep the rounded values for the merge
+            vk = rope_lanes<HD>(vk, a.rope, t, cs, sn);
+            const uint16_t kb0 = f32_to_f16_ref(vk.x), kb1 = f32_to_f16_ref(vk.y);
+            const uint16_t kb2 = f32_to_f16_ref(vk.z), kb3 = f32_to_f16_ref(vk.w);
+            const uint16_t vb0 = f32_to_f16_ref(vv.x), vb1 = f32_to_f16_ref(vv.y);
+            const uint16_t vb2 = f32_to_f16_ref(vv.z), vb3 = f32_to_f16_ref(vv.w);
+            if (hc == 0 && lane < H4) {
+                const size_t off = (size_t)a.pos * a.kv_dim + (size_t)kvh * HD + 4 * t;
+                *(u32x2*)(a.kc + off) = u32x2{kb0 | ((uint32_t)kb1 << 16), kb2 | ((uint32_t)kb3 << 16)};
+                *(u32x2*)(a.vc + off) = u32x2{vb0 | ((uint32_t)vb1 << 16), vb2 | ((uint32_t)vb3 << 16)};
             }
-    }
-    __syncthreads();
-    {
-        const int nq = cols * G * HALF;
-        const int npairs = nq + (owner ? cols * HALF : 0);
-        for (int i = tid; i < npairs; i += kDecodeThreads) {
-            const int hh = i / HALF, p = i - hh * HALF;
-            float* x = i < nq ? sqw + (size_t)hh * HD : sk[hh - cols * G];
-            int e0, e1;
-            rope_pair(a.rope, p, HD, e0, e1);
-            rope_rotate(x[e0], x[e1], s_cs[p], s_cs[HALF + p]);
-        }
-    }
-    __syncthreads();
-    if (owner) {
-        for (int i = tid; i < cols * HD; i += kDecodeThreads) {
-            const int cc = i / HD, d = i - cc * HD;
-            int kq, hq, gq;
-            col_h0(cc, kq, hq, gq);
-            const uint16_t kb = f32_to_f16_ref(sk[cc][d]);
-            const uint16_t vb = f32_to_f16_ref(sv[cc][d]);
-            if (hq == 0) {
-                const size_t off = (size_t)a.pos * a.kv_dim + (size_t)kq * HD + d;
-                a.kc[off] = kb;
-                a.vc[off] = vb;
+            if (lane < H4)
+                ((float4*)s_vnew[c])[t] = float4{f16_bits_to_f32(vb0), f16_bits_to_f32(vb1), f16_bits_to_f32(vb2),
+                                                 f16_bits_to_f32(vb3)};
+            const float k0 = f16_bits_to_f32(kb0), k1 = f16_bits_to_f32(kb1);
+            const float k2 = f16_bits_to_f32(kb2), k3 = f16_bits_to_f32(kb3);
+#pragma unroll
+            for (int r = 0; r < QL; r++) {
+                float d = vq[r].x * k0 + vq[r].y * k1 + vq[r].z * k2 + vq[r].w * k3;
+                d = group_sum<H4>(d);
+                const int hh = (lane + 64 * r) / H4;
+                if (t == 0 && hh < Gc) s_new[c][hh] = d;
             }
-            sk[cc][d] = f16_bits_to_f32(kb);
-            sv[cc][d] = f16_bits_to_f32(vb);
         }
     }
-    for (int i = tid; i < NW * G * HD; i += kDecodeThreads) sqw[i] *= a.qscale;
-    __syncthreads();
-    if (owner && tid < cols * G) {
-        const int cc = tid / G, h = tid - cc * G;
-        float s = 0.0f;
-        for (int d = 0; d < HD; d++) s = fmaf(sqw[(size_t)tid * HD + d], sk[cc][d], s);
-        s_new[cc][h] = s;
-    }
+    wave_sync();
 
     // ---------------- wave loop over history rows ----------------
     // Lane (g, n), g = lane/16, n = lane%16. The score MFMA reads K row n of the
@@ -263,17 +244,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     // lane group g also loads V rows 4g..4g+3, so each group runs its own
     // online softmax over its rows: no cross-group traffic per tile.
     half8 qh[KS], ql[KS];
+    {
+        const float* qrow = q_lds + min(n, Gc - 1) * QS + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
+        for (int ks = 0; ks < KS; ks++) {
+            const float4 x0 = *(const float4*)(qrow + 32 * ks);
+            const float4 x1 = *(const float4*)(qrow + 32 * ks + 4);
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float x = n < G ? sqw[(size_t)(c * G + n) * HD + 32 * ks + 8 * grp + e] : 0.0f;
-            const _Float16 hi = (_Float16)x;
-            qh[ks][e] = hi;
-            ql[ks][e] = (_Float16)(x - (float)hi);
+            for (int e = 0; e < 8; e++) {
+                const float xv = n < Gc ? x[e] : 0.0f;
+                const _Float16 hi = (_Float16)xv;
+                qh[ks][e] = hi;
+                ql[ks][e] = (_Float16)(xv - (float)hi);
+            }
         }
     }
-    __syncthreads();  // sqw is reused below for the wave partials
+    wave_sync();  // q_lds is reused below for the wave partial
 
     float m_run = NEG_INF;
     float l_run = 0.0f;
@@ -335,39 +322,40 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             }
         };
 
-        for (int tb = w0; tb < w1; tb += 32) {
-            process(tb, kA, vA);
-            load_tile(tb + 32, kA, vA);
-            if (tb + 16 >= w1) break;
-            process(tb + 16, kB, vB);
-            load_tile(tb + 48, kB, vB);
+        for (int tb = w0; tb < w1; tb += 16 * NT) {
+#pragma unroll
+            for (int b = 0; b < NT; b++) {
+                if (tb + 16 * b >= w1) break;
+                process(tb + 16 * b, kt[b], vt[b]);
+                load_tile(tb + 16 * (b + NT), kt[b], vt[b]);
+            }
         }
     }
 
     // ---------------- merge the four lane groups, then write the wave partial ----------------
+    // Cross-lane sums by DPP / permlane swaps: lane groups differ in lane bits
+    // 4 and 5; with HD 64 the two V rows of a lane group differ in bit 3.
     {
-        float M = fmaxf(m_run, __shfl_xor(m_run, 16));
-        M = fmaxf(M, __shfl_xor(M, 32));
+        const float M = max_x32(max_x16(m_run));
         const float e = (m_run == NEG_INF) ? 0.0f : fast_exp2(m_run - M);
-        float l = l_run * e;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        const float l = sum_x32(sum_x16(l_run * e));
 #pragma unroll
         for (int h = 0; h < G; h++) {
             const float eh = row_bcast(e, h);
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 float x = acc[h][k] * eh;
-#pragma unroll
-                for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off);
-                acc[h][k] = x;
+                if constexpr (RPG == 2) x = x + dpp_f<kDppXor8>(x);
+                acc[h][k] = sum_x32(sum_x16(x));
             }
         }
         if (lane < LPR) {
 #pragma unroll
-            for (int h = 0; h < G; h++)
-#pragma unroll
-                for (int k = 0; k < 8; k++) sqw[(size_t)(w * G + h) * HD + vdim + k] = acc[h][k];
+            for (int h = 0; h < G; h++) {
+                float* dst = q_lds + h * QS + vdim;
+                *(float4*)dst = float4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                *(float4*)(dst + 4) = float4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            }
         }
         if (lane < G) {
             wm[w][lane] = M;
@@ -377,10 +365,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     __syncthreads();
 
     // ---------------- workgroup merge per column (+ the new row) ----------------
+    const int tid = threadIdx.x;
     for (int i = tid; i < cols * G * HD; i += kDecodeThreads) {
         const int cc = i / (G * HD), h = (i / HD) - cc * G, d = i - (i / HD) * HD;
-        int kq, hq, gq;
-        const int hb = col_h0(cc, kq, hq, gq);
+        const int yk = (ybase + cc) / a.nchunk;
+        const int yc = ybase + cc - yk * a.nchunk;
+        const int gq = min(G, a.g - yc * G);
         if (h >= gq) continue;
         float M = owner ? s_new[cc][h] : NEG_INF;
         for (int s = 0; s < sub; s++) M = fmaxf(M, wm[cc + s * cols][h]);
@@ -389,15 +379,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             const int wv = cc + s * cols;
             const float e = fast_exp2(wm[wv][h] - M);
             L += e * wl[wv][h];
-            A += e * sqw[(size_t)(wv * G + h) * HD + d];
+            A += e * sq[wv][h * QS + d];
         }
         if (owner) {
             const float e = fast_exp2(s_new[cc][h] - M);
             L += e;
-            A += e * sv[cc][d];
+            A += e * s_vnew[cc][d];
         }
         if (a.nsplit == 1) {
-            a.out[(size_t)(hb + h) * HD + d] = A / L;
+            a.out[(size_t)(yk * a.g + yc * G + h) * HD + d] = A / L;
         } else {
             const size_t pb = ((size_t)(ybase + cc) * a.nsplit + split) * G + h;
             a.part_acc[pb * HD + d] = A;
@@ -407,76 +397,81 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             }
         }
     }
-    (void)h0;
 }
 
-// Merge of the split partials of one column, one workgroup per query head:
+// Merge of the split partials of one column: workgroup (head h, column y,
+// 32-dim slice). Thread (split group sg = tid / 8, float4 d4 = tid % 8) loads
+// the slice of splits sg, sg + 32, ... (at most 256 splits: one batch), and
+// thread tid the (max, sum) of split tid, all in one round trip.
 // M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s.
 // A separate launch: the kernel boundary makes every partial visible, so the
-// split workgroups need no fences or atomics. The first batch of partial
-// loads is issued together with the (max, sum) loads: one round trip when
-// nsplit <= 8 * P.
+// split workgroups need no fences or atomics.
 template <int HD>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const float* __restrict__ part_acc,
                                                                          const float* __restrict__ part_ml,
                                                                          float* __restrict__ out, int G, int g,
                                                                          int nchunk, int nsplit) {
-    constexpr int H4 = HD / 4;
-    constexpr int P = kCombineThreads / H4;  // split groups summed in parallel
-    constexpr int U = 8;                     // loads per batch per thread
+    constexpr int D4 = kCombineDims / 4;         // float4s per slice
+    constexpr int SG = kCombineThreads / D4;     // split groups
+    constexpr int U = kMaxCombineSplits / SG;    // splits per thread
+    constexpr int NWV = kCombineThreads / 64;
     constexpr float NEG_INF = -__builtin_huge_valf();
     __shared__ float s_w[kMaxCombineSplits];
-    __shared__ float s_red[kCombineThreads / 64];
-    __shared__ __attribute__((aligned(16))) floatx4 s_acc[P][H4];
+    __shared__ float s_red[2][NWV];
+    __shared__ __attribute__((aligned(16))) floatx4 s_acc[NWV][D4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int h = blockIdx.x, y = blockIdx.y;
+    const int h = blockIdx.x, y = blockIdx.y, dslice = blockIdx.z;
     const int kvh = y / nchunk, hc = y - kvh * nchunk;
     const int Gc = min(G, g - hc * G);
     if (h >= Gc) return;
     const float* pml = part_ml + ((size_t)y * nsplit * G + h) * 2;
-    const int d4 = tid % H4, pg = tid / H4;
-    const floatx4* src = (const floatx4*)(part_acc + ((size_t)y * nsplit * G + h) * HD) + d4;
-    const size_t sstride = (size_t)G * H4;
+    const int d4 = tid % D4, sg = tid / D4;
+    const floatx4* src = (const floatx4*)(part_acc + ((size_t)y * nsplit * G + h) * HD + kCombineDims * dslice) + d4;
+    const size_t sstride = (size_t)G * HD / 4;
 
     const int ts = min(tid, nsplit - 1);
-    float mloc = pml[(size_t)ts * G * 2];
-    float lloc = pml[(size_t)ts * G * 2 + 1];
+    const float2 ml = *(const float2*)(pml + (size_t)ts * G * 2);
     floatx4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) v[u] = src[(size_t)min(pg + u * P, nsplit - 1) * sstride];
-    if (tid >= nsplit) {
-        mloc = NEG_INF;
-        lloc = 0.0f;
-    }
-    float M = mloc;
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) s_red[w] = M;
+    for (int u = 0; u < U; u++) v[u] = src[(size_t)min(sg + u * SG, nsplit - 1) * sstride];
+    const float mloc = tid < nsplit ? ml.x : NEG_INF;
+    float M = group_max<64>(mloc);
+    if (lane == 0) s_red[0][w] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    M = s_red[0][0];
+#pragma unroll
+    for (int i = 1; i < NWV; i++) M = fmaxf(M, s_red[0][i]);
     float wl = 0.0f;
     if (tid < nsplit) {
         const float wt = fast_exp2(mloc - M);
         s_w[tid] = wt;
-        wl = wt * lloc;
+        wl = wt * ml.y;
     }
-    for (int off = 32; off > 0; off >>= 1) wl += __shfl_xor(wl, off);
+    wl = group_sum<64>(wl);
+    if (lane == 0) s_red[1][w] = wl;
     __syncthreads();
-    if (lane == 0) s_red[w] = wl;
-    __syncthreads();
-    const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NWV; i++) L += s_red[1][i];
     floatx4 A = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < U; u++)
-        if (pg + u * P < nsplit) A += s_w[pg + u * P] * v[u];
-    for (int sp = pg + U * P; sp < nsplit; sp += P) A += s_w[sp] * src[(size_t)sp * sstride];
-    s_acc[pg][d4] = A;
+        if (sg + u * SG < nsplit) A += s_w[sg + u * SG] * v[u];
+    // sum over the split groups of the wave (lane bits 3..5), then over waves
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float x = A[k];
+        x = x + dpp_f<kDppXor8>(x);
+        A[k] = sum_x32(sum_x16(x));
+    }
+    if (lane < D4) s_acc[w][lane] = A;
     __syncthreads();
-    if (tid < H4) {
+    if (tid < D4) {
         floatx4 r = s_acc[0][tid];
 #pragma unroll
-        for (int q = 1; q < P; q++) r += s_acc[q][tid];
+        for (int q = 1; q < NWV; q++) r += s_acc[q][tid];
         const float inv = 1.0f / L;
-        ((floatx4*)(out + (size_t)(kvh * g + hc * G + h) * HD))[tid] = r * inv;
+        ((floatx4*)(out + (size_t)(kvh * g + hc * G + h) * HD + kCombineDims * dslice))[tid] = r * inv;
     }
 }
 
@@ -510,7 +505,9 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStr
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
-    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny), dim3(kCombineThreads), 0, st, a.part_acc,
+    if (a.nsplit > kMaxCombineSplits) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(kCombineThreads), 0, st,
+                       a.part_acc,
                        a.part_ml, a.out, G, a.g, a.nchunk, a.nsplit);
     return hipGetLastError();
 }

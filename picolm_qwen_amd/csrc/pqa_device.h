@@ -129,6 +129,91 @@ __device__ __forceinline__ void pin(float4& x) {
     x = float4{v[0], v[1], v[2], v[3]};
 }
 
+// Orders the calling wave's LDS accesses before this point against those
+// after it, for data exchanged between lanes of the same wave (the LDS
+// executes one wave's requests in order; this stops the compiler moving
+// accesses across the point).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- cross-lane exchanges without LDS round trips ----
+// DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane ^ 7 within 8), row_mirror (lane ^ 15 within 16),
+// row_ror:8 (lane ^ 8 within 16).
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppXor7 = 0x141;
+constexpr int kDppXor15 = 0x140;
+constexpr int kDppXor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// gfx950 v_permlane16_swap / v_permlane32_swap with both operands = x: both
+// lanes of a pair (lane, lane ^ 16) resp. (lane, lane ^ 32) receive lo = the
+// value of the pair's lower lane and hi = that of its upper lane.
+__device__ __forceinline__ void pair16(float x, float& lo, float& hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, (unsigned)r[0]);
+    hi = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ void pair32(float x, float& lo, float& hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, (unsigned)r[0]);
+    hi = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float sum_x16(float x) {
+    float lo, hi;
+    pair16(x, lo, hi);
+    return lo + hi;
+}
+__device__ __forceinline__ float sum_x32(float x) {
+    float lo, hi;
+    pair32(x, lo, hi);
+    return lo + hi;
+}
+__device__ __forceinline__ float max_x16(float x) {
+    float lo, hi;
+    pair16(x, lo, hi);
+    return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float max_x32(float x) {
+    float lo, hi;
+    pair32(x, lo, hi);
+    return fmaxf(lo, hi);
+}
+
+// Sum / max over aligned groups of N lanes (N = 2..64) by butterflies whose
+// partner relation is symmetric, so every lane of a group ends with the same
+// bits (a + b == b + a exactly).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (N > 1) x = x + dpp_f<kDppXor1>(x);
+    if constexpr (N > 2) x = x + dpp_f<kDppXor2>(x);
+    if constexpr (N > 4) x = x + dpp_f<kDppXor7>(x);
+    if constexpr (N > 8) x = x + dpp_f<kDppXor15>(x);
+    if constexpr (N > 16) x = sum_x16(x);
+    if constexpr (N > 32) x = sum_x32(x);
+    return x;
+}
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+    if constexpr (N > 1) x = fmaxf(x, dpp_f<kDppXor1>(x));
+    if constexpr (N > 2) x = fmaxf(x, dpp_f<kDppXor2>(x));
+    if constexpr (N > 4) x = fmaxf(x, dpp_f<kDppXor7>(x));
+    if constexpr (N > 8) x = fmaxf(x, dpp_f<kDppXor15>(x));
+    if constexpr (N > 16) x = max_x16(x);
+    if constexpr (N > 32) x = max_x32(x);
+    return x;
+}
+
 // Value of lane `src` of the caller's 16-lane row (DPP row_newbcast). `src`
 // must fold to a constant after unrolling; the switch then disappears.
 template <int L>
@@ -155,6 +240,55 @@ __device__ __forceinline__ float row_bcast(float x, int src) {
         case 14: return row_bcast_c<14>(x);
         default: return row_bcast_c<15>(x);
     }
+}
+
+// RoPE of a head spread over lanes as float4s: the caller's lane holds
+// elements 4t..4t+3, t = lane mod HD/4, and every lane of the wave calls this
+// together (style is uniform). The partner of each element comes from the
+// lane that holds it: NeoX pairs (p, p + HD/2) sit HD/8 lanes apart (lane ^ 16
+// for HD 128, lane ^ 8 for HD 64), block8 pairs (8b+j, 8b+4+j) in adjacent
+// lanes (lane ^ 1), interleaved pairs inside the lane. cs/sn are the cos/sin
+// float4 at index rope_angle_f4(style, t): NeoX and block8 element e uses
+// component e, interleaved component 2(t&1) + e/2. Same roundings as
+// rope_rotate, so K rows stay bit-exact.
+template <int HD>
+__device__ __forceinline__ int rope_angle_f4(int style, int t) {
+    return style == 0 ? t % (HD / 8) : t >> 1;
+}
+
+template <int HD>
+__device__ __forceinline__ float4 rope_lanes(float4 x, int style, int t, float4 cs, float4 sn) {
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    float o[4] = {x.x, x.y, x.z, x.w};
+    const float cc[4] = {cs.x, cs.y, cs.z, cs.w};
+    const float ss[4] = {sn.x, sn.y, sn.z, sn.w};
+    if (style == 2) {
+        const int b = 2 * (t & 1);
+        rope_rotate(o[0], o[1], cc[b], ss[b]);
+        rope_rotate(o[2], o[3], cc[b + 1], ss[b + 1]);
+        return float4{o[0], o[1], o[2], o[3]};
+    }
+    float x0[4], x1[4];
+    bool first;
+    if (style == 0 && HD == 128) {
+        first = (t & 16) == 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) pair16(o[e], x0[e], x1[e]);
+    } else {
+        first = style == 0 ? (t & 8) == 0 : (t & 1) == 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float p = style == 0 ? dpp_f<kDppXor8>(o[e]) : dpp_f<kDppXor1>(o[e]);
+            x0[e] = first ? o[e] : p;
+            x1[e] = first ? p : o[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        rope_rotate(x0[e], x1[e], cc[e], ss[e]);
+        o[e] = first ? x0[e] : x1[e];
+    }
+    return float4{o[0], o[1], o[2], o[3]};
 }
 
 }  // namespace pqa
