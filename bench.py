@@ -260,6 +260,106 @@ def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
                       f"plus once on 1 thread"}
 
 
+COPY_BYTES = 1 << 30  # the calibration copy: reads and writes 1 GiB
+
+
+def pmc_probe(torch, dev):
+    """The dispatches the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)
+    count: the headline decode (36 layers x 2 steps, same cache and inputs as
+    the bench) and three launches of a plain elementwise copy of known size
+    (torch.neg over 1 GiB of fp32: 1 GiB read + 1 GiB written), whose counter
+    readings give the bytes-per-count scale."""
+    decode_workload(torch, dev, "qwen3_8b_decode", 36, 32, 8, 128, 0, 1e6, 131071, 0.01, 2, 0, True)
+    src = torch.ones(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log("[bench] pmc probe done")
+
+
+def _rows(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _find(d, suffix):
+    for root, _, files in os.walk(d):
+        for fn in files:
+            if fn.endswith(suffix):
+                return os.path.join(root, fn)
+    raise FileNotFoundError(f"no *{suffix} under {d}")
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the headline decode
+    kernels, scaled by the calibration copy's bytes per KiB counted."""
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        groups = {}
+        for r in _rows(_find(d, "counter_collection.csv")):
+            if r.get("Counter_Name") != counter:
+                continue
+            name = r["Kernel_Name"]
+            key = ("copy" if "neg_kernel" in name else "decode" if "decode_kernel<128, 4>" in name
+                   else "combine" if "decode_combine_kernel<128>" in name else None)
+            if key:
+                groups.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
+                groups[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        out[counter] = {k: (sum(v.values()) / len(v), len(v)) for k, v in groups.items()}
+    fc, _ = out["FETCH_SIZE"]["copy"]
+    wc, _ = out["WRITE_SIZE"]["copy"]
+    f_scale = COPY_BYTES / fc  # bytes per counted KiB, reads
+    w_scale = COPY_BYTES / wc
+    lines = ["kernel                              dispatches  FETCH_SIZE KiB  WRITE_SIZE KiB  read bytes     written bytes"]
+    res = {}
+    for k in ("decode", "combine", "copy"):
+        fk, nf = out["FETCH_SIZE"][k]
+        wk, _ = out["WRITE_SIZE"][k]
+        res[k] = (fk * f_scale, wk * w_scale)
+        lines.append(f"{k:36s}{nf:10d}  {fk:14.1f}  {wk:14.1f}  {fk * f_scale:13.0f}  {wk * w_scale:13.0f}")
+    alg = decode_bytes(131072, 32, 8, 128)
+    traffic = res["decode"][0] + res["decode"][1] + res["combine"][0] + res["combine"][1]
+    lines += ["",
+              f"scale: reads {f_scale:.1f} B per FETCH_SIZE KiB, writes {w_scale:.1f} B per WRITE_SIZE KiB "
+              f"(calibration copy: {COPY_BYTES} B read + {COPY_BYTES} B written per dispatch)",
+              f"algorithmic bytes per decode launch: {alg}",
+              f"hbm_traffic_bytes_per_launch: {traffic:.0f}",
+              f"traffic / algorithmic: {traffic / alg:.4f}"]
+    return "\n".join(lines)
+
+
+def summarize_trace(trace_dir):
+    """Average kernel durations per (kernel, grid) from a rocprofv3
+    --kernel-trace CSV, labelled with the workload each instance belongs to."""
+    groups = {}
+    for r in _rows(_find(trace_dir, "kernel_trace.csv")):
+        name = r["Kernel_Name"]
+        if not name.startswith("void pqa::"):
+            continue
+        grid = tuple(int(r.get(f"Grid_Size_{a}", r.get("Grid_Size", 0)) or 0) for a in "XYZ")
+        g = groups.setdefault((name, grid), [])
+        g.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"{'kernel':52s} {'grid (threads)':>20s} {'calls':>7s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}"]
+    for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        short = name.replace("void pqa::", "").split("(")[0]
+        lines.append(f"{short:52s} {str(grid):>20s} {len(d):7d} {sum(d) / len(d):9.2f} {min(d):9.2f} {max(d):9.2f}")
+    return "\n".join(lines)
+
+
+def profile_value(fname, key):
+    """A figure recorded in a committed rocprofv3 summary under profiles/
+    (None when the summary is absent)."""
+    path = os.path.join(ROOT, "profiles", fname)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(key):
+            return line
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,7 +367,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc))
+        return
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(decode would shard by KV head with no exchange; see DESIGN.md)", file=sys.stderr)
@@ -277,6 +386,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.pmc_probe:
+        pmc_probe(torch, dev)
+        return
 
     nh, nkv, hd, layers, pos = 32, 8, 128, 36, 131071
     head, cx, bufs = decode_workload(torch, dev, "qwen3_8b_decode", layers, nh, nkv, hd, 0, 1e6, pos, 0.01,
@@ -300,6 +412,17 @@ def main():
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]
+    tline = profile_value("decode_qwen3_8b_ctx131072_hbm_traffic.txt", "hbm_traffic_bytes_per_launch:")
+    traffic = int(float(tline.split(":")[1])) if tline else None
+    if "qwen3_4b_prefill" in workloads:
+        aline = profile_value("prefill_qwen3_4b_2048_kernel_trace.txt", "prefill_attn_kernel")
+        if aline:
+            attn_us = float(aline.split()[-3])
+            tf = prefill_flops(32, 128, 2048) / (attn_us * 1e-6) / 1e12
+            workloads["qwen3_4b_prefill"]["attention_only_rocprof"] = {
+                "us_per_layer": attn_us, "TFLOP_per_s": round(tf, 1),
+                "mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
+                "source": "profiles/prefill_qwen3_4b_2048_kernel_trace.txt"}
     line = {
         "metric": METRIC,
         "value": achieved,
@@ -318,9 +441,11 @@ def main():
                    "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "layers": layers, "ctx": pos + 1,
                    "kv_cache_GB": round(2 * layers * (pos + 1) * nkv * hd * 2 / 1e9, 2), "parallelism": "none"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_kernel<128,4>", "us_per_launch": per_layer_us,
-                     "bytes_per_launch": head["bytes_per_layer"]},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "decode_kernel<128,4> + decode_combine_kernel<128> (one pqa_decode call)",
+                     "us_per_launch": per_layer_us, "bytes_per_launch": head["bytes_per_layer"],
+                     "traffic_source": "profiles/decode_qwen3_8b_ctx131072_hbm_traffic.txt (rocprofv3 --pmc "
+                                       "FETCH_SIZE, WRITE_SIZE; copy-calibrated)"},
         "cpu_baseline": cpu,
         "workloads": workloads,
     }
