@@ -368,6 +368,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
+    ap.add_argument("--only", choices=["qwen3_1.7b_decode", "qwen3_4b_prefill", "tinyllama_decode",
+                                       "qwen2.5_0.5b_sweep"], help="run one secondary workload and print it")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
     args = ap.parse_args()
@@ -388,6 +390,18 @@ def main():
     dev = torch.device("cuda:0")
     if args.pmc_probe:
         pmc_probe(torch, dev)
+        return
+    if args.only:
+        runs = {
+            "qwen3_1.7b_decode": lambda: decode_workload(torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6,
+                                                         32767, 0.0, args.steps, args.warmup, True)[0],
+            "qwen3_4b_prefill": lambda: prefill_workload(torch, dev, 36, 32, 8, 128, 2048,
+                                                         max(3, args.steps // 5), 1),
+            "tinyllama_decode": lambda: decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
+                                                        0.0, max(args.steps, 200), args.warmup, False)[0],
+            "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev),
+        }
+        print(json.dumps({args.only: runs[args.only]()}), flush=True)
         return
 
     nh, nkv, hd, layers, pos = 32, 8, 128, 36, 131071

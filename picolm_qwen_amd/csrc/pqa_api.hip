@@ -33,7 +33,7 @@ static void free_ctx(pqa_ctx* c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm,
-                    c->part_acc,  c->part_ml,   c->q16,      c->stage};
+                    c->part_acc,  c->part_ml,   c->stage};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -158,18 +158,6 @@ extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, cons
     return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out), "pqa_decode");
 }
 
-static int ensure_q16(pqa_ctx* ctx, int n_tok) {
-    if ((size_t)n_tok <= ctx->q16_tokens) return PQA_OK;
-    if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), "pqa_prefill")) return rc;
-    if (ctx->q16) (void)hipFree(ctx->q16);
-    ctx->q16 = nullptr;
-    ctx->q16_tokens = 0;
-    const size_t want = std::max<size_t>((size_t)n_tok, 256);
-    if (int rc = hip_check(ctx, dev_alloc(&ctx->q16, 2 * want * ctx->q_dim), "pqa_prefill: q staging")) return rc;
-    ctx->q16_tokens = want;
-    return PQA_OK;
-}
-
 extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q, const float* k,
                            const float* v, float* out) {
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_prefill: ctx is NULL");
@@ -179,7 +167,6 @@ extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, co
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill: positions out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: NULL buffer");
     if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: buffers must be 16-byte aligned");
-    if (int rc = ensure_q16(ctx, n_tok)) return rc;
     return hip_check(ctx, pqa::launch_prefill(ctx, layer, start_pos, n_tok, q, k, v, out), "pqa_prefill");
 }
 

@@ -29,10 +29,7 @@ struct pqa_ctx {
     int split_override = 0;
     int cu_count = 256;
 
-    // prefill: normed, roped, scaled q in fp16, [tokens][n_heads][head_dim],
-    // followed by the same-sized low part when prefill_split_q is set
-    _Float16* q16 = nullptr;
-    size_t q16_tokens = 0;
+    // prefill: q = fp16 hi + lo in the score products (outlier-heavy caches)
     int prefill_split_q = 0;
 
     // staging for the _host entry points
