@@ -140,6 +140,37 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A pointer the caller knows to be wave-uniform, moved to scalar registers.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const unsigned long long v = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (const void*)(((unsigned long long)hi << 32) | lo);
+}
+
+// Byte address in LDS of a pointer into a __shared__ object (take it once,
+// outside loops: the generic -> LDS conversion carries a null check).
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at LDS byte address
+// lds + 16 l. base and lds must be wave-uniform; voff is the lane's byte
+// offset from base. Issued from inline asm on purpose: the compiler then does
+// not track the LDS write, so it does not make every later LDS read wait for
+// this load (the callers order these loads against reads of the same bytes
+// with an explicit s_waitcnt vmcnt(0) and a barrier, and never read a buffer
+// that has a load in flight).
+__device__ __forceinline__ void lds_dma_b128(const void* base, unsigned voff, unsigned lds) {
+    base = uniform_ptr(base);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
 // ---- cross-lane exchanges without LDS round trips ----
 // DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
 // row_half_mirror (lane ^ 7 within 8), row_mirror (lane ^ 15 within 16),

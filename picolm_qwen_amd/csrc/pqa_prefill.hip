@@ -101,7 +101,8 @@ struct AttnArgs {
     float qscale;
 };
 
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 512;  // 2 groups of 4 waves: even and odd key tiles
+constexpr int kGroupWaves = 4;
 constexpr int kRowsPerBlock = 128;
 constexpr int kKeysPerTile = 64;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P stays <= 256 between rescales
@@ -120,7 +121,7 @@ struct PrefillTile {
     static constexpr int ROWB = HD * 2;          // bytes per row
     static constexpr int BYTES = kKeysPerTile * ROWB;
     static constexpr int RPI = 1024 / ROWB;      // rows per 1 KB wave-wide load
-    static constexpr int NI = BYTES / 1024 / (kAttnThreads / 64);  // loads per wave per tile and operand
+    static constexpr int NI = BYTES / 1024 / kGroupWaves;  // loads per wave per tile and operand
     __device__ static int swz_k(int r) { return r & (CH - 1); }
     __device__ static int swz_v(int r) { return (4 * (r & 3)) & (CH - 1); }
 };
@@ -128,33 +129,33 @@ struct PrefillTile {
 // SPLITQ: scores use q = hi + lo (two fp16 MFMAs into one fp32 accumulator),
 // which keeps fp32-level score precision when keys carry large outliers.
 template <int HD, bool SPLITQ>
-__global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const AttnArgs a) {
     using T = PrefillTile<HD>;
     constexpr int QK = HD / 16;  // k-steps of S^T = K Q^T
     constexpr int DT = HD / 32;  // 32-dim tiles of O^T
     constexpr float NEG_INF = -__builtin_huge_valf();
-    __shared__ __attribute__((aligned(1024))) char lds[2][2][T::BYTES];  // [buffer][K, V]
+    __shared__ __attribute__((aligned(1024))) char lds[2][2][2][T::BYTES];  // [buffer][tile parity][K, V]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = w % kGroupWaves;   // row group: rows 32 wr .. 32 wr + 31 of the block
+    const int par = w / kGroupWaves;  // key tiles 2 step + par
     const int col = lane & 31;  // q row within the wave / MFMA row index
     const int hk = lane >> 5;   // MFMA k-group
     // Work item: all blocks of one KV head run on the same XCD (workgroups go
-    // round-robin over the 8 XCDs), keeping that head's K/V in one L2. Within a
-    // head, the first half of the items are the long causal blocks in
-    // decreasing length, the second half the short ones in increasing length,
-    // so the two workgroups a CU receives add up to about the same work.
+    // round-robin over the 8 XCDs), keeping that head's K/V in one L2; blocks
+    // are issued longest first, so the dispatcher hands the short ones to the
+    // CUs that finish early. Inside the workgroup the two waves of a SIMD
+    // (w and w + 4) own the same rows and alternate key tiles: equal work.
     const int kvh = (int)blockIdx.x % a.n_kv;
-    const int jj = (int)blockIdx.x / a.n_kv;
-    const int half = (a.nblk + 1) / 2;
-    const int b = jj < half ? a.nblk - 1 - jj : jj - half;
+    const int b = a.nblk - 1 - (int)blockIdx.x / a.n_kv;
 
     const char* kbase = (const char*)(a.kc + (size_t)kvh * HD);
     const char* vbase = (const char*)(a.vc + (size_t)kvh * HD);
     const size_t rowb = (size_t)a.kv_dim * 2;  // bytes per cache row
 
-    const int R0 = b * kRowsPerBlock + w * 32;
+    const int R0 = b * kRowsPerBlock + wr * 32;
     const int R = R0 + col;
     const bool rvalid = R < a.rows;
     const int tok = rvalid ? R / a.g : 0;
@@ -167,12 +168,13 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
     const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
 
     // ---- per-lane offsets, fixed for the whole loop ----
-    // global -> LDS: wave load i of an operand fills LDS bytes [1024 (w NI + i), +1024):
-    // tile row r = (w NI + i) RPI + lane / CH, source chunk (lane % CH) ^ swz(r)
+    // global -> LDS: the waves of group par load tile 2 step + par; wave load i
+    // of an operand fills LDS bytes [1024 (wr NI + i), +1024): tile row
+    // r = (wr NI + i) RPI + lane / CH, source chunk (lane % CH) ^ swz(r)
     unsigned gk[T::NI], gv[T::NI];
 #pragma unroll
     for (int i = 0; i < T::NI; i++) {
-        const int r = (w * T::NI + i) * T::RPI + lane / T::CH;
+        const int r = (wr * T::NI + i) * T::RPI + lane / T::CH;
         const int p = lane % T::CH;
         gk[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_k(r));
         gv[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_v(r));
@@ -192,30 +194,31 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
         voff[dt] = (4 * hk + tr_e) * T::ROWB + 16 * (c ^ T::swz_v(tr_e)) + 8 * (tr_q & 1);
     }
 
-    auto issue = [&](int kt, int buf) {
+    auto issue = [&](int step, int buf) {
+        const int kt = 2 * step + par;
+        if (kt >= ntiles) return;
         const int key0 = kt * kKeysPerTile;
         if (key0 + kKeysPerTile <= kend) {
             const char* kb = kbase + (size_t)key0 * rowb;
             const char* vb = vbase + (size_t)key0 * rowb;
 #pragma unroll
             for (int i = 0; i < T::NI; i++) {
-                const int inst = w * T::NI + i;
-                __builtin_amdgcn_global_load_lds((const void*)(kb + gk[i]),
-                                                 (__attribute__((address_space(3))) void*)&lds[buf][0][inst * 1024], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(vb + gv[i]),
-                                                 (__attribute__((address_space(3))) void*)&lds[buf][1][inst * 1024], 16, 0, 0);
+                const int inst = wr * T::NI + i;
+                lds_dma_b128(kb, gk[i], lds_addr(&lds[buf][par][0][inst * 1024]));
+                lds_dma_b128(vb, gv[i], lds_addr(&lds[buf][par][1][inst * 1024]));
             }
         } else {  // last tile: rows past kend (never read unmasked) clamp to kend - 1
+            const char* kb = kbase + (size_t)key0 * rowb;
+            const char* vb = vbase + (size_t)key0 * rowb;
+            const int rmax = kend - 1 - key0;
 #pragma unroll
             for (int i = 0; i < T::NI; i++) {
-                const int inst = w * T::NI + i;
+                const int inst = wr * T::NI + i;
                 const int r = inst * T::RPI + lane / T::CH;
                 const int p = lane % T::CH;
-                const size_t row = (size_t)min(key0 + r, kend - 1) * rowb;
-                __builtin_amdgcn_global_load_lds((const void*)(kbase + row + 16 * (p ^ T::swz_k(r))),
-                                                 (__attribute__((address_space(3))) void*)&lds[buf][0][inst * 1024], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(vbase + row + 16 * (p ^ T::swz_v(r))),
-                                                 (__attribute__((address_space(3))) void*)&lds[buf][1][inst * 1024], 16, 0, 0);
+                const unsigned row = (unsigned)(min(r, rmax) * rowb);
+                lds_dma_b128(kb, row + 16u * (p ^ T::swz_k(r)), lds_addr(&lds[buf][par][0][inst * 1024]));
+                lds_dma_b128(vb, row + 16u * (p ^ T::swz_v(r)), lds_addr(&lds[buf][par][1][inst * 1024]));
             }
         }
     };
@@ -225,21 +228,41 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
     // ---- q fragments: lane (col, hk) holds dims 16 ks + 8 hk + e of row col ----
     // One round trip: the q row slice, the RoPE cos/sin values it needs and
     // (direct to LDS) the norm weights are all requested with tile 0.
-    __shared__ __attribute__((aligned(16))) float s_qw[HD];
+    // The scaled fp16 q of each row group lives in LDS (sq) instead of 32
+    // registers per lane (the registers go to operand prefetch rings below);
+    // row col's 16-byte chunk c sits at slot c ^ (col mod chunks per row), so
+    // the fragment reads are conflict-free. Until sq is written the same
+    // space holds the norm weights.
+    __shared__ __attribute__((aligned(16))) char sq[kGroupWaves][32 * HD * 2];
+    float* s_qw = (float*)&sq[0][0];
     if (w == 0 && lane < HD / 4)
-        __builtin_amdgcn_global_load_lds((const void*)((a.qn ? a.qn : a.wpad) + 4 * lane),
-                                         (__attribute__((address_space(3))) void*)s_qw, 16, 0, 0);
-    half8 qf[QK], qfl[SPLITQ ? QK : 1];
-    {
-        const float* qrow = a.q + ((size_t)tok * a.nh + hq) * HD + 8 * hk;
-        float x[QK][8];
+        lds_dma_b128(a.qn ? a.qn : a.wpad, 16u * lane, lds_addr(s_qw));
+    // The q rows of this row group go to LDS (buffer 1, free until the loop)
+    // by direct loads, whole 512-byte rows per lane group: coalesced, unlike
+    // fragment-shaped loads (one row per lane, 32 rows per instruction).
+    // Lane l of a load fetches the global chunk whose swizzled slot is l, so
+    // the fragment reads below are conflict-free.
+    constexpr int CQ = HD / 4;          // 16-byte chunks per fp32 q row
+    constexpr int RPQ = 1024 / (HD * 4);  // rows per 1 KB wave load
+    constexpr int NQ = 32 / RPQ / 2;    // loads per wave (the two waves of a row group split them)
+    char* qst = &lds[1][0][0][0] + wr * 32 * HD * 4;
+    const int tq0 = min(R0, a.rows - 1) / a.g;  // first token of the row group
+    const char* qbase = (const char*)(a.q + (size_t)tq0 * a.nh * HD);
 #pragma unroll
-        for (int ks = 0; ks < QK; ks++) {
-            const float4 u0 = *(const float4*)(qrow + 16 * ks);
-            const float4 u1 = *(const float4*)(qrow + 16 * ks + 4);
-            x[ks][0] = u0.x, x[ks][1] = u0.y, x[ks][2] = u0.z, x[ks][3] = u0.w;
-            x[ks][4] = u1.x, x[ks][5] = u1.y, x[ks][6] = u1.z, x[ks][7] = u1.w;
-        }
+    for (int i = 0; i < NQ; i++) {
+        const int j = par * NQ + i;
+        const int rr = j * RPQ + lane / CQ;
+        const int Rq = min(R0 + rr, a.rows - 1);
+        const int tq = Rq / a.g;
+        const unsigned qoff = (unsigned)((((tq - tq0) * a.nh + kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
+        const int c = (lane % CQ) ^ (rr & (CQ - 1));
+        lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
+    }
+    half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode
+    const char* sq_row = sq[wr] + col * HD * 2;
+    auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
+    {
+        float x[QK][8];
         // cos/sin float4 i: NeoX angles 16 (i/2) + 8 hk + 4 (i%2) (dims of ks = i/2 < QK/2);
         // block8 / interleaved angles 4 (2 i + hk) (8-dim chunk 2 i + hk)
         const float* crow = a.cos_tab + (size_t)qpos * (HD / 2);
@@ -252,7 +275,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
             sf[i] = *(const float4*)(srow + ai);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // s_qw landed
+        __syncthreads();  // q rows and s_qw landed
+#pragma unroll
+        for (int ks = 0; ks < QK; ks++) {
+            // dims 16 ks + 8 hk + 4 j = chunk 4 ks + 2 hk + j of row col
+            const char* rowp = qst + col * HD * 4;
+            const float4 u0 = *(const float4*)(rowp + 16 * ((4 * ks + 2 * hk) ^ (col & (CQ - 1))));
+            const float4 u1 = *(const float4*)(rowp + 16 * ((4 * ks + 2 * hk + 1) ^ (col & (CQ - 1))));
+            x[ks][0] = u0.x, x[ks][1] = u0.y, x[ks][2] = u0.z, x[ks][3] = u0.w;
+            x[ks][4] = u1.x, x[ks][5] = u1.y, x[ks][6] = u1.z, x[ks][7] = u1.w;
+        }
         if (a.qn) {
             float ss = 0.0f;
 #pragma unroll
@@ -297,47 +329,78 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
             }
         }
         const float qs = rvalid ? a.qscale : 0.0f;
+        __syncthreads();  // every wave is done with the norm weights in sq
 #pragma unroll
-        for (int ks = 0; ks < QK; ks++)
+        for (int ks = 0; ks < QK; ks++) {
+            half8 hi8;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float xs = x[ks][e] * qs;
                 const _Float16 hi = (_Float16)xs;
-                qf[ks][e] = hi;
+                hi8[e] = hi;
                 if constexpr (SPLITQ) qfl[ks][e] = (_Float16)(xs - (float)hi);
             }
+            if (par == 0) *(half8*)(sq[wr] + col * HD * 2 + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))) = hi8;
+        }
     }
 
-    float m_run = NEG_INF, l_run = 0.0f;
+    // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
+    // a row whose keys in a tile are all masked (the odd group's first tile
+    // can be) then gets p = exp2(-inf) = 0 and a rescale factor of 1, never
+    // exp2(-inf - -inf).
+    float m_run = -1e30f, l_run = 0.0f;
     floatx16 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
 
-    auto tile = [&](int kt, auto BUF) {
+    auto tile = [&](int step, auto BUF) {
         constexpr int buf = decltype(BUF)::value;
+        const int kt = 2 * step + par;
         const int key0 = kt * kKeysPerTile;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of tile kt
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of step `step`
         __syncthreads();                                   // everyone's; the other buffer is free
-        if (kt + 1 < ntiles) issue(kt + 1, buf ^ 1);
-        if (key0 >= kend_w) return;  // wave-uniform: every row of this wave is done
+        issue(step + 1, buf ^ 1);
+        if (kt >= ntiles || key0 >= kend_w) return;  // wave-uniform: nothing left for this wave
 
-        const char* kt_lds = lds[buf][0];
-        const char* vt_lds = lds[buf][1];
+        const char* kt_lds = lds[buf][par][0];
+        const char* vt_lds = lds[buf][par][1];
+        // S^T = K Q^T: k-step ks takes q(ks) and the K fragments of both 32-key
+        // halves; operands come from LDS through a ring RS steps deep, so the
+        // reads run ahead of the MFMAs that consume them.
+        constexpr int RS = 3;
         floatx16 sacc[2];
+        half8 rq[RS], rk0[RS], rk1[RS];
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++) {
-            const char* kp = kt_lds + t2 * 32 * T::ROWB;
-            half8 kf = *(const half8*)(kp + koff[0]);
-            sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[0], floatx16{}, 0, 0, 0);
-            if constexpr (SPLITQ) sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfl[0], sacc[t2], 0, 0, 0);
+        for (int i = 0; i < RS; i++) {
+            rq[i] = qread(i);
+            rk0[i] = *(const half8*)(kt_lds + koff[i]);
+            rk1[i] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[i]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ks = 1; ks < QK; ks++) {
-                kf = *(const half8*)(kp + koff[ks]);
-                sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sacc[t2], 0, 0, 0);
-                if constexpr (SPLITQ)
-                    sacc[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfl[ks], sacc[t2], 0, 0, 0);
+        for (int ks = 0; ks < QK; ks++) {
+            const int sl = ks % RS;
+            const half8 qv = rq[sl], k0 = rk0[sl], k1 = rk1[sl];
+            if (ks + RS < QK) {
+                rq[sl] = qread(ks + RS);
+                rk0[sl] = *(const half8*)(kt_lds + koff[ks + RS]);
+                rk1[sl] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[ks + RS]);
+            }
+            // keep the reads ahead: the scheduler would otherwise sink them
+            // next to their MFMAs and expose the LDS latency again
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks == 0) {
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, floatx16{}, 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, floatx16{}, 0, 0, 0);
+            } else {
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, sacc[1], 0, 0, 0);
+            }
+            if constexpr (SPLITQ) {
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qfl[ks], sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qfl[ks], sacc[1], 0, 0, 0);
             }
         }
         // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
@@ -380,28 +443,65 @@ __global__ __launch_bounds__(kAttnThreads, 2) void prefill_attn_kernel(const Att
             for (int e = 0; e < 4; e++)
                 ps[s] = __builtin_amdgcn_fdot2(half2{pf[s][2 * e], pf[s][2 * e + 1]}, one2, ps[s], false);
         l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        // O^T += V^T P^T: 4 key steps x DT dim tiles; V^T fragments (two
+        // transposing reads each) through a ring RV MFMAs deep.
+        constexpr int NPV = 4 * DT, RV = 4;
+        auto vread = [&](int idx) {
+            const int s = idx / DT, dt = idx % DT;
+            half4 part[2];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                half4 part[2];
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const char* adr = vt_lds + voff[dt] + (16 * s + 8 * t) * T::ROWB;
-                    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) short4v*)adr);
-                    part[t] = __builtin_bit_cast(half4, raw);
-                }
-                const half8 vf = {part[0][0], part[0][1], part[0][2], part[0][3],
-                                  part[1][0], part[1][1], part[1][2], part[1][3]};
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[s], o[dt], 0, 0, 0);
+            for (int t = 0; t < 2; t++) {
+                const char* adr = vt_lds + voff[dt] + (16 * s + 8 * t) * T::ROWB;
+                const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)adr);
+                part[t] = __builtin_bit_cast(half4, raw);
             }
+            return half8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
+        };
+        half8 rv[RV];
+#pragma unroll
+        for (int i = 0; i < RV; i++) rv[i] = vread(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int idx = 0; idx < NPV; idx++) {
+            const half8 vf = rv[idx % RV];
+            if (idx + RV < NPV) rv[idx % RV] = vread(idx + RV);
+            __builtin_amdgcn_sched_barrier(0);
+            o[idx % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[idx / DT], o[idx % DT], 0, 0, 0);
         }
     };
 
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        tile(kt, std::integral_constant<int, 0>{});
-        if (kt + 1 < ntiles) tile(kt + 1, std::integral_constant<int, 1>{});
+    const int nsteps = (ntiles + 1) / 2;
+    for (int step = 0; step < nsteps; step += 2) {
+        tile(step, std::integral_constant<int, 0>{});
+        if (step + 1 < nsteps) tile(step + 1, std::integral_constant<int, 1>{});
+    }
+
+    // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
+    // LDS: [wr][MR][64 lanes] floats: o (16 DT per lane), m, l.
+    constexpr int MR = 16 * DT + 2;
+    static_assert(kGroupWaves * MR * 64 * 4 <= (int)sizeof(lds), "merge area exceeds the tile buffers");
+    __syncthreads();  // tile buffers are free
+    float* mg = (float*)&lds[0][0][0][0] + wr * MR * 64;
+    if (par == 1) {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mg[(16 * dt + r) * 64 + lane] = o[dt][r];
+        mg[(MR - 2) * 64 + lane] = m_run;
+        mg[(MR - 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (par == 1) return;
+    {
+        const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
+        const float M = fmaxf(m_run, mo);
+        const float fe = fast_exp2(m_run - M);
+        const float fo = fast_exp2(mo - M);
+        l_run = l_run * fe + lo * fo;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * fe + mg[(16 * dt + r) * 64 + lane] * fo;
     }
 
     const float l_tot = sum_x32(l_run);
