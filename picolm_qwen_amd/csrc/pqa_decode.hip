@@ -34,6 +34,8 @@
 // Lane groups are merged once per wave, waves of a column once per workgroup
 // (log-sum-exp weights); the workgroup writes the output (one split) or its
 // partial (max, sum, acc) per head, and decode_combine_kernel merges splits.
+#include <algorithm>
+
 #include "pqa_device.h"
 #include "pqa_internal.h"
 
@@ -53,7 +55,9 @@ struct DecodeArgs {
     float* out;
     float* part_acc;  // [ny][nsplit][G][HD]
     float* part_ml;   // [ny][nsplit][G][2]
+    unsigned* tickets;  // [gridDim.y] finished-split counters (zero between launches)
     int pos, g, nchunk, ny, rope, kv_dim, nsplit, rows_per_split;
+    int fused;  // the last workgroup of a column group merges the splits
     float qscale;
 };
 
@@ -63,6 +67,7 @@ constexpr int kDecodeTiles = 2;  // 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 32;  // head dims per combine workgroup
 constexpr int kMaxCombineSplits = 256;
+constexpr int kFusedWeights = 2048;  // (column, head, split) weights the in-kernel merge holds in LDS
 
 template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
@@ -365,38 +370,138 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     __syncthreads();
 
     // ---------------- workgroup merge per column (+ the new row) ----------------
+    // one float4 of head dims per thread and item
     const int tid = threadIdx.x;
-    for (int i = tid; i < cols * G * HD; i += kDecodeThreads) {
-        const int cc = i / (G * HD), h = (i / HD) - cc * G, d = i - (i / HD) * HD;
+    constexpr int D4 = HD / 4;
+    for (int i = tid; i < cols * G * D4; i += kDecodeThreads) {
+        const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
         const int yk = (ybase + cc) / a.nchunk;
         const int yc = ybase + cc - yk * a.nchunk;
         const int gq = min(G, a.g - yc * G);
         if (h >= gq) continue;
         float M = owner ? s_new[cc][h] : NEG_INF;
         for (int s = 0; s < sub; s++) M = fmaxf(M, wm[cc + s * cols][h]);
-        float L = 0.0f, A = 0.0f;
+        float L = 0.0f;
+        floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int s = 0; s < sub; s++) {
             const int wv = cc + s * cols;
             const float e = fast_exp2(wm[wv][h] - M);
             L += e * wl[wv][h];
-            A += e * sq[wv][h * QS + d];
+            A += e * *(const floatx4*)&sq[wv][h * QS + 4 * d4];
         }
         if (owner) {
             const float e = fast_exp2(s_new[cc][h] - M);
             L += e;
-            A += e * s_vnew[cc][d];
+            A += e * *(const floatx4*)&s_vnew[cc][4 * d4];
         }
         if (a.nsplit == 1) {
-            a.out[(size_t)(yk * a.g + yc * G + h) * HD + d] = A / L;
+            ((floatx4*)(a.out + (size_t)(yk * a.g + yc * G + h) * HD))[d4] = A / L;
         } else {
             const size_t pb = ((size_t)(ybase + cc) * a.nsplit + split) * G + h;
-            a.part_acc[pb * HD + d] = A;
-            if (d == 0) {
-                a.part_ml[pb * 2] = M;
-                a.part_ml[pb * 2 + 1] = L;
-            }
+            ((floatx4*)(a.part_acc + pb * HD))[d4] = A;
+            if (d4 == 0) *(float2*)(a.part_ml + pb * 2) = float2{M, L};
         }
     }
+    if (!a.fused) return;
+
+    // ---------------- last workgroup of the column group merges the splits ----------------
+    // Release: every thread's partial stores are written back to memory
+    // before thread 0 takes a ticket; the workgroup holding the last ticket
+    // invalidates its cache (acquire) and reads all splits of its columns.
+    // M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s,
+    // as decode_combine_kernel does.
+    __shared__ unsigned s_ticket;
+    __shared__ float s_cw[kFusedWeights];
+    __shared__ __attribute__((aligned(16))) float s_cl[kFusedWeights];  // later the SG partial sums (float4)
+    static_assert(kFusedWeights >= 4 * kDecodeThreads, "one float4 partial per thread");
+    __shared__ float s_cL[NW * G];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0)
+        s_ticket = __hip_atomic_fetch_add(&a.tickets[blockIdx.y], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket != (unsigned)a.nsplit - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int npair = cols * G;
+    const int ns = a.nsplit;
+    // Thread (item, split group): item = (pair, float4 of dims); the SG
+    // threads of an item take splits sg, sg + SG, ... and add up through LDS;
+    // with more items than threads SG is 1 and the items take several passes.
+    // The first pass's first FU partial loads go out before the (m, l) round
+    // trip, so the two overlap.
+    constexpr int FU = 16;
+    const int items = npair * D4;
+    const int SG = max(1, min(ns, kDecodeThreads / items));
+    const int per_pass = kDecodeThreads / SG;
+    const int sgi = tid % SG;
+    const size_t sstride = (size_t)G * HD / 4;
+    auto item_src = [&](int item) {  // (pair, float4) of an item; out-of-range items read item 0
+        const int it = item < items ? item : 0;
+        const int pr = it / D4, d4 = it - (it / D4) * D4;
+        const int pc = pr / G, ph = pr - pc * G;
+        return (const floatx4*)(a.part_acc + ((size_t)(ybase + pc) * ns * G + ph) * HD) + d4;
+    };
+    floatx4 v[FU];
+    {
+        const floatx4* src = item_src(tid / SG);
+#pragma unroll
+        for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + u * SG, ns - 1) * sstride];
+    }
+    for (int i = tid; i < npair * ns; i += kDecodeThreads) {  // (pair, split) -> m, l
+        const int p2 = i / ns, sp = i - p2 * ns;
+        const int cc = p2 / G, h = p2 - cc * G;
+        const float2 ml = *(const float2*)(a.part_ml + (((size_t)(ybase + cc) * ns + sp) * G + h) * 2);
+        s_cw[i] = ml.x;
+        s_cl[i] = ml.y;
+    }
+    __syncthreads();
+    for (int p2 = tid; p2 < npair; p2 += kDecodeThreads) {  // weights and the denominator per pair
+        float M = NEG_INF;
+        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, s_cw[p2 * ns + sp]);
+        float L = 0.0f;
+        for (int sp = 0; sp < ns; sp++) {
+            const float wt = fast_exp2(s_cw[p2 * ns + sp] - M);
+            s_cw[p2 * ns + sp] = wt;
+            L += wt * s_cl[p2 * ns + sp];
+        }
+        s_cL[p2] = L;
+    }
+    __syncthreads();
+    floatx4* red = (floatx4*)s_cl;  // the l values are used up: SG partial sums per item
+    for (int it0 = 0; it0 < items; it0 += per_pass) {
+        const int item = it0 + tid / SG;
+        const bool has = tid < per_pass * SG && item < items;
+        const int pr = has ? item / D4 : 0, d4 = has ? item - (item / D4) * D4 : 0;
+        const int nmine = has ? (ns - sgi + SG - 1) / SG : 0;
+        const floatx4* src = item_src(has ? item : 0);
+        if (it0 > 0) {
+#pragma unroll
+            for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + u * SG, ns - 1) * sstride];
+        }
+        floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < FU; u++)
+            if (u < nmine) A += s_cw[pr * ns + sgi + u * SG] * v[u];
+        for (int u0 = FU; u0 < nmine; u0 += FU) {  // more splits than one batch
+#pragma unroll
+            for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + (u0 + u) * SG, ns - 1) * sstride];
+#pragma unroll
+            for (int u = 0; u < FU; u++)
+                if (u0 + u < nmine) A += s_cw[pr * ns + sgi + (u0 + u) * SG] * v[u];
+        }
+        red[tid] = A;
+        __syncthreads();
+        if (has && sgi == 0) {
+            for (int j = 1; j < SG; j++) A += red[tid + j];
+            const int pc = pr / G, ph = pr - pc * G;
+            const int yk = (ybase + pc) / a.nchunk;
+            const int yc = ybase + pc - yk * a.nchunk;
+            if (ph < min(G, a.g - yc * G))
+                ((floatx4*)(a.out + (size_t)(yk * a.g + yc * G + ph) * HD))[d4] = A * (1.0f / s_cL[pr]);
+        }
+        __syncthreads();  // red is reused by the next pass
+    }
+    if (tid == 0) __hip_atomic_store(&a.tickets[blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge of the split partials of one column: workgroup (head h, column y,
@@ -476,19 +581,26 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
 }
 
 void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit) {
+    // Waves per column: a workgroup of 8 waves serves up to 8 columns, and
+    // each wave should own at least one whole 16-row tile.
+    const int ny = ctx->n_kv_heads * ctx->n_chunk;
+    const int cols = std::min(ny, kDecodeWaves);
+    const int quantum = 16 * (kDecodeWaves / cols);
     int rps;
     if (ctx->split_override > 0) {
         rps = ctx->split_override;
     } else {
         // About one workgroup (8 waves) per CU; a workgroup reads whole cache
         // rows of all its columns.
-        rps = (hist + ctx->cu_count - 1) / ctx->cu_count;
+        const int groups = (ny + kDecodeWaves - 1) / kDecodeWaves;
+        const int target = std::max(1, ctx->cu_count / groups);
+        rps = (hist + target - 1) / target;
+        rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
     }
-    rps = max(128, (rps + 127) & ~127);
-    int ns = max(1, (hist + rps - 1) / rps);
+    int ns = std::max(1, (hist + rps - 1) / rps);
     while (ns > ctx->max_splits) {
-        rps += 128;
-        ns = max(1, (hist + rps - 1) / rps);
+        rps += quantum;
+        ns = std::max(1, (hist + rps - 1) / rps);
     }
     *rows_per_split = rps;
     *nsplit = ns;
@@ -504,7 +616,7 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStr
         default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.nsplit == 1) return e;
+    if (e != hipSuccess || a.nsplit == 1 || a.fused) return e;
     if (a.nsplit > kMaxCombineSplits) return hipErrorInvalidValue;
     hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(kCombineThreads), 0, st,
                        a.part_acc,
@@ -537,6 +649,11 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.rope = ctx->rope_style;
     a.kv_dim = (int)ctx->kv_dim;
     decode_split(ctx, pos, &a.rows_per_split, &a.nsplit);
+    // Few splits: the last workgroup of each column group merges them in the
+    // same launch; many: a separate merge launch spreads the reads.
+    const int cols = std::min(a.ny, kDecodeWaves);
+    a.fused = a.nsplit > 1 && cols * ctx->chunk_heads * a.nsplit <= kFusedWeights;
+    a.tickets = ctx->tickets;
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid(a.nsplit, (a.ny + kDecodeWaves - 1) / kDecodeWaves);
     if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, grid, ctx->stream);

@@ -25,6 +25,7 @@ CASES = [
     ("interleaved_g1", 8, 8, 64, 300, 2, 1e4, False, 299, 0.0),
     ("block8_g3_qknorm", 12, 4, 128, 200, 1, 1e4, True, 150, 0.0),
     ("g5_pos_65", 10, 2, 64, 100, 0, 1e6, True, 65, 0.0),
+    ("two_column_groups", 32, 16, 64, 400, 0, 1e6, False, 333, 0.0),
 ]
 
 
@@ -117,3 +118,30 @@ def test_decode_host_and_device_paths_agree():
             outs.append(o.cpu().numpy())
         att.close()
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_decode_successive_positions():
+    # One context, token after token: the in-kernel split merge hands its
+    # completion counter back to zero for the next call, and each call sees
+    # the rows the previous calls appended.
+    nh, nkv, hd, smax, pos0, n = 32, 4, 64, 640, 600, 6
+    seed = 9100
+    cos, sin = O.rope_table(1e4, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, 1, rope_cos=cos, rope_sin=sin)
+    att.synth_kv(0, 0, pos0, seed, 0.0)
+    kh, vh = O.synth_kv_rows(seed, 0, nkv * hd, 0, pos0, 0.0, cpu_threads())
+    kc = np.zeros((smax, nkv * hd), np.uint16)
+    vc = np.zeros((smax, nkv * hd), np.uint16)
+    kc[:pos0], vc[:pos0] = kh, vh
+    shp = O.shape(nh, nkv, hd, smax, 1)
+    for i in range(n):
+        pos = pos0 + i
+        print(f"decode successive pos {pos}", flush=True)
+        q, k, v = O.step_inputs(seed, 0, i, nh, nkv, hd)
+        got = att.forward(0, pos, q, k, v)
+        want = O.attn_step(shp, pos, q, k, v, None, None, cos[pos], sin[pos], kc, vc, cpu_threads())
+        assert_close(got, want)
+    gk, gv = att.kv_download(0, pos0, n)
+    assert_bits_equal(gk, kc[pos0:pos0 + n], "appended K rows")
+    assert_bits_equal(gv, vc[pos0:pos0 + n], "appended V rows")
+    att.close()
