@@ -58,6 +58,7 @@ struct DecodeArgs {
     unsigned* tickets;  // [gridDim.y] finished-split counters (zero between launches)
     int pos, g, nchunk, ny, rope, kv_dim, nsplit, rows_per_split;
     int fused;  // the last workgroup of a column group merges the splits
+    int cpw;    // columns per workgroup: 8 (whole cache rows) or 1 (short histories)
     float qscale;
 };
 
@@ -68,6 +69,8 @@ constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 32;  // head dims per combine workgroup
 constexpr int kMaxCombineSplits = 256;
 constexpr int kFusedWeights = 2048;  // (column, head, split) weights the in-kernel merge holds in LDS
+constexpr int kFusedSplits = 64;     // splits the in-kernel merge takes (one lane each)
+constexpr int kShortRowsPerWave = 64;  // per-column workgroups: history rows per wave
 
 template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
@@ -97,8 +100,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int split = blockIdx.x;
-    const int ybase = blockIdx.y * NW;
-    const int cols = min(a.ny - ybase, NW);
+    const int ybase = blockIdx.y * a.cpw;
+    const int cols = min(a.ny - ybase, a.cpw);
     const int sub = NW / cols;
     const bool active = w < cols * sub;
     const int c = active ? w % cols : 0;
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     // as decode_combine_kernel does.
     __shared__ unsigned s_ticket;
     __shared__ float s_cw[kFusedWeights];
-    __shared__ __attribute__((aligned(16))) float s_cl[kFusedWeights];  // later the SG partial sums (float4)
+    __shared__ __attribute__((aligned(16))) float s_cl[kFusedWeights];  // the SG partial sums (float4)
     static_assert(kFusedWeights >= 4 * kDecodeThreads, "one float4 partial per thread");
     __shared__ float s_cL[NW * G];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -447,27 +450,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 #pragma unroll
         for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + u * SG, ns - 1) * sstride];
     }
-    for (int i = tid; i < npair * ns; i += kDecodeThreads) {  // (pair, split) -> m, l
-        const int p2 = i / ns, sp = i - p2 * ns;
+    for (int p2 = w; p2 < npair; p2 += NW) {  // one wave per (column, head), one lane per split
         const int cc = p2 / G, h = p2 - cc * G;
-        const float2 ml = *(const float2*)(a.part_ml + (((size_t)(ybase + cc) * ns + sp) * G + h) * 2);
-        s_cw[i] = ml.x;
-        s_cl[i] = ml.y;
+        const bool ok = lane < ns;
+        const float2 ml = ok ? *(const float2*)(a.part_ml + (((size_t)(ybase + cc) * ns + lane) * G + h) * 2)
+                             : float2{NEG_INF, 0.0f};
+        const float M = group_max<64>(ml.x);
+        const float wt = ok ? fast_exp2(ml.x - M) : 0.0f;
+        const float L = group_sum<64>(wt * ml.y);
+        if (ok) s_cw[p2 * ns + lane] = wt;
+        if (lane == 0) s_cL[p2] = L;
     }
     __syncthreads();
-    for (int p2 = tid; p2 < npair; p2 += kDecodeThreads) {  // weights and the denominator per pair
-        float M = NEG_INF;
-        for (int sp = 0; sp < ns; sp++) M = fmaxf(M, s_cw[p2 * ns + sp]);
-        float L = 0.0f;
-        for (int sp = 0; sp < ns; sp++) {
-            const float wt = fast_exp2(s_cw[p2 * ns + sp] - M);
-            s_cw[p2 * ns + sp] = wt;
-            L += wt * s_cl[p2 * ns + sp];
-        }
-        s_cL[p2] = L;
-    }
-    __syncthreads();
-    floatx4* red = (floatx4*)s_cl;  // the l values are used up: SG partial sums per item
+    floatx4* red = (floatx4*)s_cl;  // SG partial sums per item
     for (int it0 = 0; it0 < items; it0 += per_pass) {
         const int item = it0 + tid / SG;
         const bool has = tid < per_pass * SG && item < items;
@@ -580,10 +575,24 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
     }
 }
 
-void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit) {
-    // Waves per column: a workgroup of 8 waves serves up to 8 columns, and
-    // each wave should own at least one whole 16-row tile.
+void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit, int* cols_per_wg) {
     const int ny = ctx->n_kv_heads * ctx->n_chunk;
+    if (ctx->split_override <= 0) {
+        // Short histories: one workgroup per column, its 8 waves on 64 rows
+        // each, so the history takes few splits (often one) and the chain of
+        // round trips stays short; used while these workgroups fill at most a
+        // quarter of the CUs.
+        const int rps = kDecodeWaves * kShortRowsPerWave;
+        const int ns = std::max(1, (hist + rps - 1) / rps);
+        if (ns * ny <= ctx->cu_count / 4 && ns <= kFusedSplits) {
+            *rows_per_split = rps;
+            *nsplit = ns;
+            *cols_per_wg = 1;
+            return;
+        }
+    }
+    // Whole cache rows: a workgroup of 8 waves serves up to 8 columns, and
+    // each wave should own at least one whole 16-row tile.
     const int cols = std::min(ny, kDecodeWaves);
     const int quantum = 16 * (kDecodeWaves / cols);
     int rps;
@@ -604,6 +613,7 @@ void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit
     }
     *rows_per_split = rps;
     *nsplit = ns;
+    *cols_per_wg = cols;
 }
 
 template <int HD>
@@ -648,14 +658,13 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.ny = ctx->n_kv_heads * ctx->n_chunk;
     a.rope = ctx->rope_style;
     a.kv_dim = (int)ctx->kv_dim;
-    decode_split(ctx, pos, &a.rows_per_split, &a.nsplit);
+    decode_split(ctx, pos, &a.rows_per_split, &a.nsplit, &a.cpw);
     // Few splits: the last workgroup of each column group merges them in the
     // same launch; many: a separate merge launch spreads the reads.
-    const int cols = std::min(a.ny, kDecodeWaves);
-    a.fused = a.nsplit > 1 && cols * ctx->chunk_heads * a.nsplit <= kFusedWeights;
+    a.fused = a.nsplit > 1 && a.nsplit <= kFusedSplits && a.cpw * ctx->chunk_heads * a.nsplit <= kFusedWeights;
     a.tickets = ctx->tickets;
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);
-    dim3 grid(a.nsplit, (a.ny + kDecodeWaves - 1) / kDecodeWaves);
+    dim3 grid(a.nsplit, (a.ny + a.cpw - 1) / a.cpw);
     if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, grid, ctx->stream);
     if (hd == 128) return launch_decode_hd<128>(a, ctx->chunk_heads, grid, ctx->stream);
     return hipErrorInvalidValue;

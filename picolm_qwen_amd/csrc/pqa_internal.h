@@ -26,7 +26,7 @@ struct pqa_ctx {
     float* part_acc = nullptr;      // [n_kv*n_chunk][max_splits][chunk_heads][head_dim]
     float* part_ml = nullptr;       // [n_kv*n_chunk][max_splits][chunk_heads][2]
     int max_splits = 0;
-    unsigned* tickets = nullptr;    // [column groups] finished-split counters of the in-kernel merge
+    unsigned* tickets = nullptr;    // [columns] finished-split counters of the in-kernel merge
     int split_override = 0;
     int cu_count = 256;
 
@@ -47,8 +47,9 @@ namespace pqa {
 int set_err(pqa_ctx* ctx, int code, const std::string& msg);
 int hip_check(pqa_ctx* ctx, hipError_t e, const char* what);
 
-// Rows per decode workgroup and the number of splits for `hist` history rows.
-void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit);
+// Rows per decode workgroup, the number of splits and the columns (KV head,
+// chunk) per workgroup for `hist` history rows.
+void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit, int* cols_per_wg);
 
 hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
                          const float* v, float* out);
