@@ -225,26 +225,24 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
 
     issue(0, 0);
 
-    // ---- q fragments: lane (col, hk) holds dims 16 ks + 8 hk + e of row col ----
-    // One round trip: the q row slice, the RoPE cos/sin values it needs and
-    // (direct to LDS) the norm weights are all requested with tile 0.
-    // The scaled fp16 q of each row group lives in LDS (sq) instead of 32
-    // registers per lane (the registers go to operand prefetch rings below);
-    // row col's 16-byte chunk c sits at slot c ^ (col mod chunks per row), so
-    // the fragment reads are conflict-free. Until sq is written the same
-    // space holds the norm weights.
+    // ---- q: normed, rotated, scaled, fp16, into LDS (sq) ----
+    // The q rows of the row group reach LDS (buffer 1, free until the loop)
+    // by direct loads, whole rows per lane group: coalesced, unlike
+    // fragment-shaped loads. Row r's 16-byte chunk c sits at slot c ^ (r mod
+    // chunks per row), so both the reads below and the fragment reads of the
+    // loop are conflict-free. The two waves of a row group prepare 16 rows
+    // each: lane (rr, j) = (lane / 4, lane % 4) holds of row 16 par + rr the
+    // dims j HD/8 .. +HD/8 of both halves, i.e. whole RoPE pairs of all three
+    // pairings (NeoX d ~ d + HD/2; block8 and interleaved inside 8-dim
+    // chunks), so the rotation stays in the lane and the norm is a quad sum.
+    // Until sq is written the same space holds the norm weights.
     __shared__ __attribute__((aligned(16))) char sq[kGroupWaves][32 * HD * 2];
     float* s_qw = (float*)&sq[0][0];
     if (w == 0 && lane < HD / 4)
         lds_dma_b128(a.qn ? a.qn : a.wpad, 16u * lane, lds_addr(s_qw));
-    // The q rows of this row group go to LDS (buffer 1, free until the loop)
-    // by direct loads, whole 512-byte rows per lane group: coalesced, unlike
-    // fragment-shaped loads (one row per lane, 32 rows per instruction).
-    // Lane l of a load fetches the global chunk whose swizzled slot is l, so
-    // the fragment reads below are conflict-free.
-    constexpr int CQ = HD / 4;          // 16-byte chunks per fp32 q row
+    constexpr int CQ = HD / 4;            // 16-byte chunks per fp32 q row
     constexpr int RPQ = 1024 / (HD * 4);  // rows per 1 KB wave load
-    constexpr int NQ = 32 / RPQ / 2;    // loads per wave (the two waves of a row group split them)
+    constexpr int NQ = 32 / RPQ / 2;      // loads per wave (the two waves of a row group split them)
     char* qst = &lds[1][0][0][0] + wr * 32 * HD * 4;
     const int tq0 = min(R0, a.rows - 1) / a.g;  // first token of the row group
     const char* qbase = (const char*)(a.q + (size_t)tq0 * a.nh * HD);
@@ -258,91 +256,98 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         const int c = (lane % CQ) ^ (rr & (CQ - 1));
         lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
     }
-    half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode
-    const char* sq_row = sq[wr] + col * HD * 2;
-    auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
+    constexpr int NF = HD / 16;       // float4s per lane: NF/2 in each half
+    constexpr int NH4 = NF / 2;       // float4s per half
+    const int prow = 16 * par + (lane >> 2), pj = lane & 3;
+    const int pR = R0 + prow;
+    const int pqpos = a.start + min(pR, a.rows - 1) / a.g;
+    auto pchunk = [&](int i) { return (i / NH4) * (CQ / 2) + pj * NH4 + (i % NH4); };  // fp32 chunk of float4 i
+    half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode, in the MFMA operand layout
     {
-        float x[QK][8];
-        // cos/sin float4 i: NeoX angles 16 (i/2) + 8 hk + 4 (i%2) (dims of ks = i/2 < QK/2);
-        // block8 / interleaved angles 4 (2 i + hk) (8-dim chunk 2 i + hk)
-        const float* crow = a.cos_tab + (size_t)qpos * (HD / 2);
-        const float* srow = a.sin_tab + (size_t)qpos * (HD / 2);
-        float4 cf[QK], sf[QK];
+        // cos/sin float4 q: NeoX the angles of half-0 float4 q (4 * its chunk);
+        // block8 / interleaved the four angles 2c .. 2c+3 of chunk pair (c, c+1)
+        const float* crow = a.cos_tab + (size_t)pqpos * (HD / 2);
+        const float* srow = a.sin_tab + (size_t)pqpos * (HD / 2);
+        float4 cf[NH4], sf[NH4];
 #pragma unroll
-        for (int i = 0; i < QK; i++) {
-            const int ai = a.rope == 0 ? 16 * (i >> 1) + 8 * hk + 4 * (i & 1) : 4 * (2 * i + hk);
-            cf[i] = *(const float4*)(crow + ai);
-            sf[i] = *(const float4*)(srow + ai);
+        for (int q = 0; q < NH4; q++) {
+            const int ai = a.rope == 0 ? 4 * pchunk(q) : 2 * pchunk((q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2)));
+            cf[q] = *(const float4*)(crow + ai);
+            sf[q] = *(const float4*)(srow + ai);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // q rows and s_qw landed
+        float x[NF][4];
+        const char* rowp = qst + prow * HD * 4;
 #pragma unroll
-        for (int ks = 0; ks < QK; ks++) {
-            // dims 16 ks + 8 hk + 4 j = chunk 4 ks + 2 hk + j of row col
-            const char* rowp = qst + col * HD * 4;
-            const float4 u0 = *(const float4*)(rowp + 16 * ((4 * ks + 2 * hk) ^ (col & (CQ - 1))));
-            const float4 u1 = *(const float4*)(rowp + 16 * ((4 * ks + 2 * hk + 1) ^ (col & (CQ - 1))));
-            x[ks][0] = u0.x, x[ks][1] = u0.y, x[ks][2] = u0.z, x[ks][3] = u0.w;
-            x[ks][4] = u1.x, x[ks][5] = u1.y, x[ks][6] = u1.z, x[ks][7] = u1.w;
+        for (int i = 0; i < NF; i++) {
+            const float4 u = *(const float4*)(rowp + 16 * (pchunk(i) ^ (prow & (CQ - 1))));
+            x[i][0] = u.x, x[i][1] = u.y, x[i][2] = u.z, x[i][3] = u.w;
         }
         if (a.qn) {
             float ss = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++)
+            for (int i = 0; i < NF; i++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) ss = fmaf(x[ks][e], x[ks][e], ss);
-            ss = sum_x32(ss);  // + the partner lane's 64 dims
+                for (int e = 0; e < 4; e++) ss = fmaf(x[i][e], x[i][e], ss);
+            ss = group_sum<4>(ss);  // the row's four lanes
             const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++) {
-                const float4 w0 = *(const float4*)(s_qw + 16 * ks + 8 * hk);
-                const float4 w1 = *(const float4*)(s_qw + 16 * ks + 8 * hk + 4);
-                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[ks][e] = rms_apply(x[ks][e], sc, wv[e]);
+            for (int i = 0; i < NF; i++) {
+                const float4 wv = *(const float4*)(s_qw + 4 * pchunk(i));
+                x[i][0] = rms_apply(x[i][0], sc, wv.x);
+                x[i][1] = rms_apply(x[i][1], sc, wv.y);
+                x[i][2] = rms_apply(x[i][2], sc, wv.z);
+                x[i][3] = rms_apply(x[i][3], sc, wv.w);
             }
         }
-        if (a.rope == 0) {
-            // NeoX: dim d < HD/2 pairs with d + HD/2, i.e. ks with ks + QK/2; angle d
 #pragma unroll
-            for (int ks = 0; ks < QK / 2; ks++) {
-                const float cv[8] = {cf[2 * ks].x, cf[2 * ks].y, cf[2 * ks].z, cf[2 * ks].w,
-                                     cf[2 * ks + 1].x, cf[2 * ks + 1].y, cf[2 * ks + 1].z, cf[2 * ks + 1].w};
-                const float sv[8] = {sf[2 * ks].x, sf[2 * ks].y, sf[2 * ks].z, sf[2 * ks].w,
-                                     sf[2 * ks + 1].x, sf[2 * ks + 1].y, sf[2 * ks + 1].z, sf[2 * ks + 1].w};
+        for (int q = 0; q < NH4; q++) {
+            const float cv[4] = {cf[q].x, cf[q].y, cf[q].z, cf[q].w};
+            const float sv[4] = {sf[q].x, sf[q].y, sf[q].z, sf[q].w};
+            if (a.rope == 0) {  // NeoX: float4 q of half 0 with float4 q of half 1
 #pragma unroll
-                for (int e = 0; e < 8; e++) rope_rotate(x[ks][e], x[ks + QK / 2][e], cv[e], sv[e]);
-            }
-        } else {
-            // 8-dim chunk 2 ks + hk: block8 pairs (e, e+4), interleaved pairs (2i, 2i+1)
+                for (int e = 0; e < 4; e++) rope_rotate(x[q][e], x[NH4 + q][e], cv[e], sv[e]);
+            } else {
+                const int i0 = (q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2));  // chunk pair (i0, i0 + 1)
+                if (a.rope == 1) {  // block8: element e of the two halves of the 8-dim chunk
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++) {
-                const float cv[4] = {cf[ks].x, cf[ks].y, cf[ks].z, cf[ks].w};
-                const float sv[4] = {sf[ks].x, sf[ks].y, sf[ks].z, sf[ks].w};
-                if (a.rope == 1) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) rope_rotate(x[ks][e], x[ks][e + 4], cv[e], sv[e]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) rope_rotate(x[ks][2 * e], x[ks][2 * e + 1], cv[e], sv[e]);
+                    for (int e = 0; e < 4; e++) rope_rotate(x[i0][e], x[i0 + 1][e], cv[e], sv[e]);
+                } else {  // interleaved: (2i, 2i+1), angles 2c .. 2c+3 over the chunk pair
+                    rope_rotate(x[i0][0], x[i0][1], cv[0], sv[0]);
+                    rope_rotate(x[i0][2], x[i0][3], cv[1], sv[1]);
+                    rope_rotate(x[i0 + 1][0], x[i0 + 1][1], cv[2], sv[2]);
+                    rope_rotate(x[i0 + 1][2], x[i0 + 1][3], cv[3], sv[3]);
                 }
             }
         }
-        const float qs = rvalid ? a.qscale : 0.0f;
+        const float qs = pR < a.rows ? a.qscale : 0.0f;
         __syncthreads();  // every wave is done with the norm weights in sq
+        // fp16 chunk (i0 / 2) = float4s (i0, i0 + 1); hi to sq, the residual
+        // (split-q) over the row's own fp32 staging
 #pragma unroll
-        for (int ks = 0; ks < QK; ks++) {
-            half8 hi8;
+        for (int i0 = 0; i0 < NF; i0 += 2) {
+            half8 hi8, lo8;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float xs = x[ks][e] * qs;
-                const _Float16 hi = (_Float16)xs;
-                hi8[e] = hi;
-                if constexpr (SPLITQ) qfl[ks][e] = (_Float16)(xs - (float)hi);
+                const float xs = x[i0 + e / 4][e % 4] * qs;
+                hi8[e] = (_Float16)xs;
+                lo8[e] = (_Float16)(xs - (float)hi8[e]);
             }
-            if (par == 0) *(half8*)(sq[wr] + col * HD * 2 + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))) = hi8;
+            const int slot = 16 * ((pchunk(i0) / 2) ^ (prow & (T::CH - 1)));
+            *(half8*)(sq[wr] + prow * HD * 2 + slot) = hi8;
+            if constexpr (SPLITQ) *(half8*)(qst + prow * HD * 4 + slot) = lo8;
+        }
+        if constexpr (SPLITQ) {
+            __syncthreads();  // both waves' residual rows landed
+            const char* lrow = qst + col * HD * 4;
+#pragma unroll
+            for (int ks = 0; ks < QK; ks++)
+                qfl[ks] = *(const half8*)(lrow + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1))));
         }
     }
+    const char* sq_row = sq[wr] + col * HD * 2;
+    auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
 
     // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
     // a row whose keys in a tile are all masked (the odd group's first tile

@@ -24,6 +24,8 @@ CASES = [
     ("g2_n77", 16, 8, 128, 128, 0, 1e6, True, 0, 77, 0.0),
     ("g16_n40", 32, 2, 128, 128, 2, 1e4, True, 10, 40, 0.0),
     ("g1_interleaved_n65", 4, 4, 64, 96, 2, 1e4, False, 0, 65, 0.0),
+    ("block8_hd128_splitq_n150", 16, 4, 128, 200, 1, 1e4, True, 3, 150, 0.01),
+    ("interleaved_hd64_splitq_n130", 8, 2, 64, 160, 2, 1e4, True, 0, 130, 0.01),
 ]
 
 
