@@ -85,13 +85,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     constexpr int QS = HD + 4;        // padded LDS row stride of a head
     constexpr float NEG_INF = -__builtin_huge_valf();
 
-    // Per wave: its column's q heads ([G][QS], raw, then normalised, rotated
-    // and scaled), later the wave's partial accumulator. Per wave: the K row
-    // for the exact norm and the norm scales. Per column: the new row's V and
-    // scores. Every region but the last three is private to one wave.
+    // Per wave: its column's q heads ([G][QS], normalised, rotated and
+    // scaled), later the wave's partial accumulator; the new K row for the
+    // exact norm. Per column: the new row's V and scores. Every region but
+    // the last three is private to one wave.
     __shared__ __attribute__((aligned(16))) float sq[NW][G * QS];
     __shared__ __attribute__((aligned(16))) float skr[NW][HD];
-    __shared__ float s_scale[NW][G + 1];
     __shared__ __attribute__((aligned(16))) float s_vnew[NW][HD];
     __shared__ float s_new[NW][G];
     __shared__ float wm[NW][G];
@@ -178,30 +177,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 
     float* q_lds = sq[w];
     if (active) {
-        // QK-RMSNorm scales in the reference's summation order: quad j of lane
-        // 4h+j sums x[j], x[j+4], ... sequentially (heads h < Gc, then the K row).
+        // QK-RMSNorm. q only feeds scores: an fp32 tree sum over the head's
+        // H4 lanes. K is stored, so its scale follows the reference's
+        // summation order (cpp/tensor.hpp:146-176): quad j sums x[j], x[j+4],
+        // ... sequentially; only the wave that appends the new row needs it.
         if (a.qn) {
 #pragma unroll
             for (int r = 0; r < QL; r++) {
-                const int i = lane + 64 * r;
-                if (i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
-            }
-            if (writer && lane < H4) ((float4*)skr[w])[t] = vk;
-            wave_sync();
-            const int qd = lane >> 2;
-            const bool is_k = qd == Gc;
-            const float* src = is_k ? skr[w] : q_lds + min(qd, Gc - 1) * QS;
-            const float s = rms_scale_ref_quad(src, HD, lane & 3);
-            if ((lane & 3) == 0 && (qd < Gc || (is_k && writer))) s_scale[w][qd] = s;
-            wave_sync();
-#pragma unroll
-            for (int r = 0; r < QL; r++) {
-                const float sc = s_scale[w][min((lane + 64 * r) / H4, Gc - 1)];
+                const float ss = group_sum<H4>(vq[r].x * vq[r].x + vq[r].y * vq[r].y + vq[r].z * vq[r].z +
+                                               vq[r].w * vq[r].w);
+                const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
                 vq[r] = float4{rms_apply(vq[r].x, sc, wq.x), rms_apply(vq[r].y, sc, wq.y),
                                rms_apply(vq[r].z, sc, wq.z), rms_apply(vq[r].w, sc, wq.w)};
             }
             if (writer) {
-                const float sc = s_scale[w][Gc];
+                if (lane < H4) ((float4*)skr[w])[t] = vk;
+                wave_sync();
+                const float sc = rms_scale_ref_quad(skr[w], HD, lane & 3);
                 vk = float4{rms_apply(vk.x, sc, wk.x), rms_apply(vk.y, sc, wk.y), rms_apply(vk.z, sc, wk.z),
                             rms_apply(vk.w, sc, wk.w)};
             }
