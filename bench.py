@@ -14,6 +14,7 @@ Also reported in the same JSON line under "workloads":
   qwen3_4b_prefill    32/8/128, 2048-token causal prefill, 36 layers (MFMA)
   tinyllama_decode    32/4/64, block8 RoPE, pos 511, 1 layer (latency)
   qwen2.5_0.5b_sweep  14/2/64, positions 0..4095 token by token, 24 layers
+  qwen3_8b_kvc_save_load  .kvc save/load of 4096 positions x 36 layers (604 MB)
 
 `roofline` covers the decode kernel of the headline workload, timed with HIP
 events on the library's stream. `cpu_baseline` times the CPU oracle (the
@@ -217,6 +218,71 @@ def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096,
             "avg_us_per_layer_launch_loop": round(avg_us, 3), "us_per_layer_vs_ctx": curve}
 
 
+def kvc_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n_pos=4096, reps=3):
+    """.kvc persistence (picolm/model.c:870-983) of a Qwen3-8B-shaped cache
+    prefix, 4096 positions x 36 layers (604 MB file): pqa_kvc_save /
+    pqa_kvc_load between HBM and a file in the temp directory (page cache, no
+    fsync, as the reference), beside the reference's own kvcache_save /
+    kvcache_load (oracle/_ref/libref_kvc.so, where built) on a host copy of
+    the same cache. Unit: file GB/s, median of `reps` after one warm-up."""
+    import filecmp
+    import tempfile
+    import oracle as O
+    cx = Ctx(n_layers, n_pos, nh, nkv, hd, 0, 1e6)
+    for layer in range(n_layers):
+        cx.check(cx.L.pqa_synth_kv(cx.h, layer, 0, n_pos, 1234 + layer, 0.0), cx.h)
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    kv_dim = nkv * hd
+    nbytes = 16 + 2 * n_layers * n_pos * kv_dim * 2
+    tmp = tempfile.mkdtemp(prefix="pqa_kvc_")
+    ours = os.path.join(tmp, "ours.kvc")
+    ref = os.path.join(tmp, "ref.kvc")
+
+    def clock(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def save():
+        cx.check(cx.L.pqa_kvc_save(cx.h, ours.encode(), n_pos), cx.h)
+
+    def load():
+        if cx.L.pqa_kvc_load(cx.h, ours.encode()) != n_pos:
+            raise RuntimeError(cx.L.pqa_last_error(cx.h))
+
+    res = {"workload": "qwen3_8b_kvc_save_load", "n_layers": n_layers, "n_pos": n_pos, "kv_dim": kv_dim,
+           "file_bytes": nbytes, "unit": "GB/s (file bytes / wall time)"}
+    try:
+        t_save, t_load = clock(save), clock(load)
+        res.update(save_GB_per_s=round(nbytes / t_save / 1e9, 3), load_GB_per_s=round(nbytes / t_load / 1e9, 3),
+                   save_ms=round(t_save * 1e3, 2), load_ms=round(t_load * 1e3, 2))
+        if O.RefKvc.available():
+            kc = np.zeros((n_layers, n_pos, kv_dim), np.uint16)
+            vc = np.zeros((n_layers, n_pos, kv_dim), np.uint16)
+            for layer in range(n_layers):
+                cx.check(cx.L.pqa_kv_download(cx.h, layer, 0, n_pos, kc[layer].ctypes.data_as(C.c_void_p),
+                                              vc[layer].ctypes.data_as(C.c_void_p)), cx.h)
+            r_save = clock(lambda: O.RefKvc.save(kc, vc, nkv, hd, ref, n_pos))
+            r_load = clock(lambda: O.RefKvc.load_into(kc, vc, nkv, hd, ref))
+            res["cpu_baseline"] = {
+                "kind": "reference", "cores": 1,
+                "save_GB_per_s": round(nbytes / r_save / 1e9, 3), "load_GB_per_s": round(nbytes / r_load / 1e9, 3),
+                "sample": "kvcache_save / kvcache_load of the same cache bytes from host memory, same file size"}
+            res["files_identical"] = filecmp.cmp(ours, ref, shallow=False)
+    finally:
+        for f in (ours, ref):
+            if os.path.exists(f):
+                os.unlink(f)
+        os.rmdir(tmp)
+        cx.close()
+    log(f"[bench] kvc: {res}")
+    return res
+
+
 def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
     """The oracle (reference attention loop, restated in C) on layer 0 of the
     headline cache: same K/V bytes (downloaded), same q/k/v and norm weights."""
@@ -369,7 +435,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
     ap.add_argument("--only", choices=["qwen3_1.7b_decode", "qwen3_4b_prefill", "tinyllama_decode",
-                                       "qwen2.5_0.5b_sweep"], help="run one secondary workload and print it")
+                                       "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load"],
+                    help="run one secondary workload and print it")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
     args = ap.parse_args()
@@ -400,6 +467,7 @@ def main():
             "tinyllama_decode": lambda: decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
                                                         0.0, max(args.steps, 200), args.warmup, False)[0],
             "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev),
+            "qwen3_8b_kvc_save_load": lambda: kvc_workload(torch, dev),
         }
         print(json.dumps({args.only: runs[args.only]()}), flush=True)
         return
@@ -423,6 +491,7 @@ def main():
         workloads["tinyllama_decode"] = decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
                                                         0.0, max(args.steps, 200), args.warmup, False)[0]
         workloads["qwen2.5_0.5b_sweep"] = sweep_workload(torch, dev)
+        workloads["qwen3_8b_kvc_save_load"] = kvc_workload(torch, dev)
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]

@@ -35,6 +35,8 @@ extern "C" {
 #define PQA_ERR_UNSUPPORTED (-3) /* head_dim not in {64, 128} */
 #define PQA_ERR_HIP (-4)         /* a HIP runtime call failed */
 #define PQA_ERR_NOMEM (-5)       /* device allocation failed */
+#define PQA_ERR_IO (-6)          /* a .kvc file could not be opened, read or written */
+#define PQA_ERR_FORMAT (-7)      /* a .kvc file has a bad magic or another model's shape */
 
 typedef struct pqa_ctx pqa_ctx;
 
@@ -104,6 +106,35 @@ int pqa_kv_download(pqa_ctx* ctx, int layer, int pos0, int n, uint16_t* k_rows, 
 
 /* Device base pointers of the whole cache ([n_layers][max_seq_len][kv_dim]). */
 int pqa_kv_cache(pqa_ctx* ctx, uint16_t** key_cache, uint16_t** val_cache);
+
+/*
+ * KV-cache persistence in the reference's .kvc format, so files written by
+ * either side load in the other (picolm/model.c:870-983, declared
+ * picolm/model.h:156-164, called picolm/picolm.c:266-293,:364-367):
+ *   uint32 {0x4B564350 "KVCP", n_pos, n_layers, kv_dim} in host byte order,
+ *   then K rows [0, n_pos) of layer 0, 1, ..., then V rows the same way,
+ *   kv_dim fp16 per row.
+ * Both stream the HBM cache through two pinned host buffers (16 MiB each,
+ * made on first use) and are synchronous: the cache state is the one the
+ * context stream has reached when the call is made.
+ *
+ * pqa_kvc_save replaces kvcache_save (picolm/model.c:882-921). Returns PQA_OK,
+ * PQA_ERR_RANGE for n_pos outside [1, max_seq_len] (no file is created, the
+ * reference's -1 case), PQA_ERR_IO when the file cannot be opened or a write
+ * fails (the reference does not check its writes). Prints nothing.
+ */
+int pqa_kvc_save(pqa_ctx* ctx, const char* path, int n_pos);
+
+/*
+ * pqa_kvc_load replaces kvcache_load (picolm/model.c:923-983) with its
+ * return contract: the header's position count on success, 0 on any failure
+ * (missing file, short header, bad magic, n_layers or kv_dim other than the
+ * context's, more positions than max_seq_len, a file that ends early), with
+ * the reason in pqa_last_error. As in the reference, a file that ends early
+ * leaves the bytes it did hold in the cache, and a header count of 2^31 or
+ * more comes back negative with nothing loaded.
+ */
+int pqa_kvc_load(pqa_ctx* ctx, const char* path);
 
 /* The context's HIP stream (a hipStream_t), for event timing or ordering. */
 void* pqa_stream(pqa_ctx* ctx);

@@ -18,7 +18,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
-REF_SO = {"A": os.path.join(HERE, "_ref", "libref_A.so"), "B": os.path.join(HERE, "_ref", "libref_B.so")}
+REF_SO = {"A": os.path.join(HERE, "_ref", "libref_A.so"), "B": os.path.join(HERE, "_ref", "libref_B.so"),
+          "kvc": os.path.join(HERE, "_ref", "libref_kvc.so")}
 
 ROPE_NEOX_HALF, ROPE_LLAMA_X86_BLOCK8, ROPE_LLAMA_INTERLEAVED = 0, 1, 2
 KIND_Q, KIND_K, KIND_V, KIND_KHIST, KIND_VHIST, KIND_QNORM, KIND_KNORM, KIND_OUTLIER = range(1, 9)
@@ -326,3 +327,97 @@ class RefModel:
             self.close()
         except Exception:
             pass
+
+
+# ---- .kvc KV-cache files (picolm/model.c:870-983) ----------------------------
+#
+# Restated with numpy on whole caches [n_layers][max_seq_len][kv_dim] uint16.
+# Pinned in tests/test_oracle_kvc.py against the reference's compiled
+# kvcache_save / kvcache_load (RefKvc below) on every branch of both, against
+# a committed file written by kvcache_save, and against the format's closed
+# form (length 16 + 4*n_layers*n_pos*kv_dim, the magic bytes "PCVK" on disk).
+
+KVC_MAGIC = 0x4B564350  # picolm/model.h:12
+
+
+def kvc_file_bytes(key_cache, val_cache, n_pos):
+    """kvcache_save (picolm/model.c:882-921): the file for rows [0, n_pos).
+    Returns None where the reference returns -1 without writing (n_pos outside
+    [1, max_seq_len])."""
+    n_layers, max_seq_len, kv_dim = key_cache.shape
+    if n_pos <= 0 or n_pos > max_seq_len:
+        return None
+    header = np.array([KVC_MAGIC, n_pos, n_layers, kv_dim], dtype="<u4")      # :895-901
+    body_k = np.ascontiguousarray(key_cache[:, :n_pos], dtype="<u2")            # :905-910
+    body_v = np.ascontiguousarray(val_cache[:, :n_pos], dtype="<u2")            # :911-916
+    return header.tobytes() + body_k.tobytes() + body_v.tobytes()
+
+
+def kvc_load_bytes(data, key_cache, val_cache):
+    """kvcache_load (picolm/model.c:923-983) of file contents `data` into the
+    caches, in place. Returns what the reference returns: the header's n_pos
+    (an int32, so a count of 2^31 or more is negative and loads nothing), or 0
+    on a short header, bad magic, shape mismatch, n_pos > max_seq_len or a
+    short body; a short body leaves the bytes it held in place, as the
+    row-by-row fread does (:961-978)."""
+    n_layers, max_seq_len, kv_dim = key_cache.shape
+    if len(data) < 16:                                                          # :932-935
+        return 0
+    magic, n_pos_u, file_layers, file_kv_dim = np.frombuffer(data[:16], dtype="<u4").tolist()
+    to_i32 = lambda u: u - (1 << 32) if u >= (1 << 31) else u
+    n_pos, file_layers, file_kv_dim = to_i32(n_pos_u), to_i32(file_layers), to_i32(file_kv_dim)
+    if magic != KVC_MAGIC:                                                      # :937-941
+        return 0
+    if file_layers != n_layers or file_kv_dim != kv_dim:                        # :947-952
+        return 0
+    if n_pos > max_seq_len:                                                     # :953-958
+        return 0
+    if n_pos <= 0:
+        return n_pos
+    body = memoryview(data)[16:]
+    run = n_pos * kv_dim * 2
+    off = 0
+    for cache in (key_cache, val_cache):
+        flat = cache.reshape(n_layers, -1).view(np.uint8)
+        for layer in range(n_layers):
+            take = max(0, min(run, len(body) - off))
+            flat[layer, :take] = np.frombuffer(body[off:off + take], dtype=np.uint8)
+            off += take
+            if take < run:
+                return 0
+    return n_pos
+
+
+class RefKvc:
+    """The reference's kvcache_save / kvcache_load via oracle/ref_kvc_harness.c."""
+
+    _lib = None
+
+    @classmethod
+    def available(cls):
+        return os.path.exists(REF_SO["kvc"])
+
+    @classmethod
+    def load(cls):
+        if cls._lib is None:
+            L = C.CDLL(REF_SO["kvc"])
+            args = [_u16p, _u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_char_p]
+            L.refkvc_save.argtypes = args + [C.c_int]
+            L.refkvc_load.argtypes = args
+            cls._lib = L
+        return cls._lib
+
+    @classmethod
+    def save(cls, key_cache, val_cache, n_kv_heads, head_dim, path, n_pos):
+        n_layers, max_seq_len, _ = key_cache.shape
+        return cls.load().refkvc_save(np.ascontiguousarray(key_cache, np.uint16),
+                                      np.ascontiguousarray(val_cache, np.uint16), n_layers, max_seq_len,
+                                      n_kv_heads, head_dim, os.fsencode(path), n_pos)
+
+    @classmethod
+    def load_into(cls, key_cache, val_cache, n_kv_heads, head_dim, path):
+        """Loads in place (caches must be C-contiguous uint16)."""
+        assert key_cache.flags.c_contiguous and val_cache.flags.c_contiguous
+        n_layers, max_seq_len, _ = key_cache.shape
+        return cls.load().refkvc_load(key_cache, val_cache, n_layers, max_seq_len, n_kv_heads, head_dim,
+                                      os.fsencode(path))

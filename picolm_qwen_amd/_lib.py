@@ -13,12 +13,14 @@ PQA_ERR_RANGE = -2
 PQA_ERR_UNSUPPORTED = -3
 PQA_ERR_HIP = -4
 PQA_ERR_NOMEM = -5
+PQA_ERR_IO = -6
+PQA_ERR_FORMAT = -7
 
 EXPORTS = [
     "pqa_create", "pqa_set_qk_norm", "pqa_decode", "pqa_prefill", "pqa_decode_host",
     "pqa_prefill_host", "pqa_kv_upload", "pqa_kv_download", "pqa_kv_cache", "pqa_stream",
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
-    "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision",
+    "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
 ]
 
 
@@ -62,6 +64,8 @@ def lib() -> C.CDLL:
     L.pqa_synth_kv.argtypes = [vp, i, i, i, u64, f]
     L.pqa_set_decode_split.argtypes = [vp, i]
     L.pqa_set_prefill_precision.argtypes = [vp, i]
+    L.pqa_kvc_save.argtypes = [vp, C.c_char_p, i]
+    L.pqa_kvc_load.argtypes = [vp, C.c_char_p]
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int

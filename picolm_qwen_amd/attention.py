@@ -17,6 +17,7 @@ goes through libpqa.so; a missing library raises.
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import numpy as np
 
@@ -218,6 +219,19 @@ class PicoAttention:
         kp, vp = C.c_void_p(), C.c_void_p()
         check(lib().pqa_kv_cache(self.handle, C.byref(kp), C.byref(vp)), self.handle)
         return kp.value, vp.value
+
+    # -- .kvc persistence (picolm/model.c:870-983) ---------------------------
+    def kvc_save(self, path: str, n_pos: int) -> None:
+        """kvcache_save: rows [0, n_pos) of every layer to `path`; raises PQAError."""
+        check(lib().pqa_kvc_save(self.handle, os.fsencode(path), n_pos), self.handle)
+
+    def kvc_load(self, path: str) -> int:
+        """kvcache_load: the file's position count, 0 on failure (reason in last_error())."""
+        return lib().pqa_kvc_load(self.handle, os.fsencode(path))
+
+    def last_error(self) -> str:
+        msg = lib().pqa_last_error(self.handle)
+        return msg.decode() if msg else ""
 
     def synth_kv(self, layer: int, pos0: int, n: int, seed: int, outlier_prob: float = 0.0) -> None:
         """Seeded synthetic history rows (same generator as the CPU oracle)."""

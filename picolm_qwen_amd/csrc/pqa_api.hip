@@ -36,6 +36,10 @@ static void free_ctx(pqa_ctx* c) {
                     c->part_acc,  c->part_ml,   c->stage,   c->tickets};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    for (int i = 0; i < 2; ++i) {
+        if (c->kvc_buf[i]) (void)hipHostFree(c->kvc_buf[i]);
+        if (c->kvc_ev[i]) (void)hipEventDestroy(c->kvc_ev[i]);
+    }
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }

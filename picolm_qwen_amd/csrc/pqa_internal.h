@@ -37,6 +37,11 @@ struct pqa_ctx {
     float* stage = nullptr;
     size_t stage_floats = 0;
 
+    // .kvc file streaming: two pinned host buffers and their copy events,
+    // made on the first pqa_kvc_save / pqa_kvc_load
+    void* kvc_buf[2] = {nullptr, nullptr};
+    hipEvent_t kvc_ev[2] = {nullptr, nullptr};
+
     hipStream_t stream = nullptr;
     int device = 0;
     std::string err;

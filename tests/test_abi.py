@@ -54,6 +54,9 @@ def test_null_context_calls_fail_cleanly():
     assert L.pqa_decode(None, 0, 0, None, None, None, None) == _lib.PQA_ERR_ARG
     assert L.pqa_prefill(None, 0, 0, 1, None, None, None, None) == _lib.PQA_ERR_ARG
     assert L.pqa_sync(None) == _lib.PQA_ERR_ARG
+    assert L.pqa_kvc_save(None, b"/nonexistent/x.kvc", 1) == _lib.PQA_ERR_ARG
+    assert L.pqa_kvc_load(None, b"/nonexistent/x.kvc") == 0
+    assert b"ctx is NULL" in L.pqa_last_error(None)
     assert L.pqa_stream(None) is None
     L.pqa_destroy(None)
 
