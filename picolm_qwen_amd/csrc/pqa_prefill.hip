@@ -8,21 +8,23 @@
 // 2. prefill_attn: flash attention over the fp16 cache on
 //    v_mfma_f32_32x32x16_f16. The query heads of one KV head are packed as
 //    rows R = token*g + h (g = query heads per KV head), so one K/V tile in
-//    LDS serves the whole GQA group. A workgroup is 4 waves x 32 packed rows.
-//    Each wave first builds its q fragments in registers from the fp32
-//    projections: in the MFMA operand layout a lane holds 64 of its row's
-//    dims and every RoPE pair of all three pairings lies inside the lane, so
-//    norm (one exchange with the partner lane) and rotation need no LDS.
-//    Per 64-key tile each wave computes S^T = K Q^T (keys x rows), the online
-//    softmax per row (a lane owns one row: its 32 scores plus the partner
-//    lane 32 apart), and O^T += V^T P^T. With S^T in the MFMA result layout
-//    the lane's scores are already the B operand of the PV product, so P
-//    never leaves registers. The running maximum is raised (and O, l
-//    rescaled) only when a score exceeds it by more than 2^8, so most tiles
-//    skip the rescale. K/V tiles arrive by direct global->LDS loads, double
-//    buffered, one barrier per tile; V fragments are read with transposing
-//    LDS reads. Tiles past the causal limit of every row in a wave are
-//    skipped.
+//    LDS serves the whole GQA group. A workgroup of 8 waves takes a pair of
+//    128-row blocks one after the other (a long and a short one, so every
+//    workgroup has the same causal work). Waves w and w + 4 share a SIMD and
+//    32 rows and take the even and the odd 64-key tiles; their partial
+//    results are merged at the end of the block.
+//    Per block: q rows are normed, rotated, scaled and rounded to fp16 into
+//    LDS (each lane holds whole RoPE pairs of its row, so the rotation needs
+//    no exchange). Per 64-key tile each wave computes S^T = K Q^T (keys x
+//    rows), the online softmax per row (a lane owns one row: its 32 scores
+//    plus the partner lane 32 apart), and O^T += V^T P^T. With S^T in the
+//    MFMA result layout the lane's scores are already the B operand of the
+//    PV product, so P never leaves registers. The running maximum is raised
+//    (and O, l rescaled) only when a score exceeds it by more than 2^8, so
+//    most tiles skip the rescale. K/V tiles arrive by direct global->LDS
+//    loads, double buffered, one barrier per tile pair; V fragments are read
+//    with transposing LDS reads. Tiles past the causal limit of every row in
+//    a wave are skipped. Outputs leave through LDS as whole 512-byte rows.
 #include <type_traits>
 
 #include "pqa_device.h"
@@ -141,386 +143,422 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = w % kGroupWaves;   // row group: rows 32 wr .. 32 wr + 31 of the block
     const int par = w / kGroupWaves;  // key tiles 2 step + par
-    const int col = lane & 31;  // q row within the wave / MFMA row index
-    const int hk = lane >> 5;   // MFMA k-group
-    // Work item: all blocks of one KV head run on the same XCD (workgroups go
-    // round-robin over the 8 XCDs), keeping that head's K/V in one L2; blocks
-    // are issued longest first, so the dispatcher hands the short ones to the
-    // CUs that finish early. Inside the workgroup the two waves of a SIMD
+    // Work item: a pair of row blocks of one KV head, the longest remaining
+    // (nblk - 1 - i) and then the shortest (i), so that every workgroup has
+    // about the same work and the second block's prologue runs while the
+    // first block's output stores drain. The pairs of one KV head run on the
+    // same XCD (workgroups go round-robin over the 8 XCDs), keeping that
+    // head's K/V in one L2. Inside the workgroup the two waves of a SIMD
     // (w and w + 4) own the same rows and alternate key tiles: equal work.
     const int kvh = (int)blockIdx.x % a.n_kv;
-    const int b = a.nblk - 1 - (int)blockIdx.x / a.n_kv;
+    const int pair = (int)blockIdx.x / a.n_kv;
+    const int nb = a.nblk - 1 - pair == pair ? 1 : 2;
 
     const char* kbase = (const char*)(a.kc + (size_t)kvh * HD);
     const char* vbase = (const char*)(a.vc + (size_t)kvh * HD);
     const size_t rowb = (size_t)a.kv_dim * 2;  // bytes per cache row
 
-    const int R0 = b * kRowsPerBlock + wr * 32;
-    const int R = R0 + col;
-    const bool rvalid = R < a.rows;
-    const int tok = rvalid ? R / a.g : 0;
-    const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
-    const int qpos = a.start + tok;
-    const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
-    const int kend = a.start + last_row_blk / a.g + 1;
-    const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
-    const int kend_w = R0 < a.rows ? a.start + (min(a.rows, R0 + 32) - 1) / a.g + 1 : 0;
-    const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
-
-    // ---- per-lane offsets, fixed for the whole loop ----
-    // global -> LDS: the waves of group par load tile 2 step + par; wave load i
-    // of an operand fills LDS bytes [1024 (wr NI + i), +1024): tile row
-    // r = (wr NI + i) RPI + lane / CH, source chunk (lane % CH) ^ swz(r)
-    unsigned gk[T::NI], gv[T::NI];
-#pragma unroll
-    for (int i = 0; i < T::NI; i++) {
-        const int r = (wr * T::NI + i) * T::RPI + lane / T::CH;
-        const int p = lane % T::CH;
-        gk[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_k(r));
-        gv[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_v(r));
-    }
-    // K fragment reads: row 32 t2 + col, chunk (2 ks + hk) ^ swz_k(col)
-    int koff[QK];
-#pragma unroll
-    for (int ks = 0; ks < QK; ks++) koff[ks] = col * T::ROWB + 16 * ((2 * ks + hk) ^ T::swz_k(col));
-    // V^T fragment reads (transposing): row 16 s + 8 t + 4 hk + tr_e,
-    // dims 32 dt + 16 (g16 & 1) + 4 tr_q .. +3
-    const int j16 = lane & 15, g16 = lane >> 4;
-    const int tr_e = j16 >> 2, tr_q = j16 & 3;
-    int voff[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        const int c = 4 * dt + 2 * (g16 & 1) + (tr_q >> 1);
-        voff[dt] = (4 * hk + tr_e) * T::ROWB + 16 * (c ^ T::swz_v(tr_e)) + 8 * (tr_q & 1);
-    }
-
-    auto issue = [&](int step, int buf) {
-        const int kt = 2 * step + par;
-        if (kt >= ntiles) return;
-        const int key0 = kt * kKeysPerTile;
-        if (key0 + kKeysPerTile <= kend) {
-            const char* kb = kbase + (size_t)key0 * rowb;
-            const char* vb = vbase + (size_t)key0 * rowb;
-#pragma unroll
-            for (int i = 0; i < T::NI; i++) {
-                const int inst = wr * T::NI + i;
-                lds_dma_b128(kb, gk[i], lds_addr(&lds[buf][par][0][inst * 1024]));
-                lds_dma_b128(vb, gv[i], lds_addr(&lds[buf][par][1][inst * 1024]));
-            }
-        } else {  // last tile: rows past kend (never read unmasked) clamp to kend - 1
-            const char* kb = kbase + (size_t)key0 * rowb;
-            const char* vb = vbase + (size_t)key0 * rowb;
-            const int rmax = kend - 1 - key0;
-#pragma unroll
-            for (int i = 0; i < T::NI; i++) {
-                const int inst = wr * T::NI + i;
-                const int r = inst * T::RPI + lane / T::CH;
-                const int p = lane % T::CH;
-                const unsigned row = (unsigned)(min(r, rmax) * rowb);
-                lds_dma_b128(kb, row + 16u * (p ^ T::swz_k(r)), lds_addr(&lds[buf][par][0][inst * 1024]));
-                lds_dma_b128(vb, row + 16u * (p ^ T::swz_v(r)), lds_addr(&lds[buf][par][1][inst * 1024]));
-            }
-        }
-    };
-
-    issue(0, 0);
-
-    // ---- q: normed, rotated, scaled, fp16, into LDS (sq) ----
-    // The q rows of the row group reach LDS (buffer 1, free until the loop)
-    // by direct loads, whole rows per lane group: coalesced, unlike
-    // fragment-shaped loads. Row r's 16-byte chunk c sits at slot c ^ (r mod
-    // chunks per row), so both the reads below and the fragment reads of the
-    // loop are conflict-free. The two waves of a row group prepare 16 rows
-    // each: lane (rr, j) = (lane / 4, lane % 4) holds of row 16 par + rr the
-    // dims j HD/8 .. +HD/8 of both halves, i.e. whole RoPE pairs of all three
-    // pairings (NeoX d ~ d + HD/2; block8 and interleaved inside 8-dim
-    // chunks), so the rotation stays in the lane and the norm is a quad sum.
-    // Until sq is written the same space holds the norm weights.
+    // q of the current block, normed, rotated, scaled, fp16 (see below)
     __shared__ __attribute__((aligned(16))) char sq[kGroupWaves][32 * HD * 2];
-    float* s_qw = (float*)&sq[0][0];
-    if (w == 0 && lane < HD / 4)
-        lds_dma_b128(a.qn ? a.qn : a.wpad, 16u * lane, lds_addr(s_qw));
-    constexpr int CQ = HD / 4;            // 16-byte chunks per fp32 q row
-    constexpr int RPQ = 1024 / (HD * 4);  // rows per 1 KB wave load
-    constexpr int NQ = 32 / RPQ / 2;      // loads per wave (the two waves of a row group split them)
-    char* qst = &lds[1][0][0][0] + wr * 32 * HD * 4;
-    const int tq0 = min(R0, a.rows - 1) / a.g;  // first token of the row group
-    const char* qbase = (const char*)(a.q + (size_t)tq0 * a.nh * HD);
+
+    for (int j = 0; j < nb; j++) {
+        const int b = j == 0 ? a.nblk - 1 - pair : pair;
+        if (j) __syncthreads();  // the previous block's epilogue is done with the LDS
+
+        // Lane-derived offsets are rebuilt for each block (the empty asm hides
+        // that the lane id is loop-invariant), so they are not held live, and
+        // spilled, across the whole pair.
+        int lane_j = tid & 63;
+        asm volatile("" : "+v"(lane_j));
+        const int lane = lane_j;
+        const int col = lane & 31;
+        const int hk = lane >> 5;
+
+        // ---- per-lane offsets, fixed for the block's tile loop ----
+        // global -> LDS: the waves of group par load tile 2 step + par; wave load i
+        // of an operand fills LDS bytes [1024 (wr NI + i), +1024): tile row
+        // r = (wr NI + i) RPI + lane / CH, source chunk (lane % CH) ^ swz(r)
+        unsigned gk[T::NI], gv[T::NI];
 #pragma unroll
-    for (int i = 0; i < NQ; i++) {
-        const int j = par * NQ + i;
-        const int rr = j * RPQ + lane / CQ;
-        const int Rq = min(R0 + rr, a.rows - 1);
-        const int tq = Rq / a.g;
-        const unsigned qoff = (unsigned)((((tq - tq0) * a.nh + kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
-        const int c = (lane % CQ) ^ (rr & (CQ - 1));
-        lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
-    }
-    constexpr int NF = HD / 16;       // float4s per lane: NF/2 in each half
-    constexpr int NH4 = NF / 2;       // float4s per half
-    const int prow = 16 * par + (lane >> 2), pj = lane & 3;
-    const int pR = R0 + prow;
-    const int pqpos = a.start + min(pR, a.rows - 1) / a.g;
-    auto pchunk = [&](int i) { return (i / NH4) * (CQ / 2) + pj * NH4 + (i % NH4); };  // fp32 chunk of float4 i
-    half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode, in the MFMA operand layout
-    {
-        // cos/sin float4 q: NeoX the angles of half-0 float4 q (4 * its chunk);
-        // block8 / interleaved the four angles 2c .. 2c+3 of chunk pair (c, c+1)
-        const float* crow = a.cos_tab + (size_t)pqpos * (HD / 2);
-        const float* srow = a.sin_tab + (size_t)pqpos * (HD / 2);
-        float4 cf[NH4], sf[NH4];
-#pragma unroll
-        for (int q = 0; q < NH4; q++) {
-            const int ai = a.rope == 0 ? 4 * pchunk(q) : 2 * pchunk((q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2)));
-            cf[q] = *(const float4*)(crow + ai);
-            sf[q] = *(const float4*)(srow + ai);
+        for (int i = 0; i < T::NI; i++) {
+            const int r = (wr * T::NI + i) * T::RPI + lane / T::CH;
+            const int p = lane % T::CH;
+            gk[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_k(r));
+            gv[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_v(r));
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // q rows and s_qw landed
-        float x[NF][4];
-        const char* rowp = qst + prow * HD * 4;
+        // K fragment reads: row 32 t2 + col, chunk (2 ks + hk) ^ swz_k(col)
+        int koff[QK];
 #pragma unroll
-        for (int i = 0; i < NF; i++) {
-            const float4 u = *(const float4*)(rowp + 16 * (pchunk(i) ^ (prow & (CQ - 1))));
-            x[i][0] = u.x, x[i][1] = u.y, x[i][2] = u.z, x[i][3] = u.w;
+        for (int ks = 0; ks < QK; ks++) koff[ks] = col * T::ROWB + 16 * ((2 * ks + hk) ^ T::swz_k(col));
+        // V^T fragment reads (transposing): row 16 s + 8 t + 4 hk + tr_e,
+        // dims 32 dt + 16 (g16 & 1) + 4 tr_q .. +3
+        const int j16 = lane & 15, g16 = lane >> 4;
+        const int tr_e = j16 >> 2, tr_q = j16 & 3;
+        int voff[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int c = 4 * dt + 2 * (g16 & 1) + (tr_q >> 1);
+            voff[dt] = (4 * hk + tr_e) * T::ROWB + 16 * (c ^ T::swz_v(tr_e)) + 8 * (tr_q & 1);
         }
-        if (a.qn) {
-            float ss = 0.0f;
+
+        const int R0 = b * kRowsPerBlock + wr * 32;
+        const int R = R0 + col;
+        const bool rvalid = R < a.rows;
+        const int tok = rvalid ? R / a.g : 0;
+        const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
+        const int qpos = a.start + tok;
+        const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
+        const int kend = a.start + last_row_blk / a.g + 1;
+        const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
+        const int kend_w = R0 < a.rows ? a.start + (min(a.rows, R0 + 32) - 1) / a.g + 1 : 0;
+        const int qpos_min_w = R0 < a.rows ? a.start + R0 / a.g : 0;
+
+        auto issue = [&](int step, int buf) {
+            const int kt = 2 * step + par;
+            if (kt >= ntiles) return;
+            const int key0 = kt * kKeysPerTile;
+            const char* kb = kbase + (size_t)key0 * rowb;
+            const char* vb = vbase + (size_t)key0 * rowb;
+            if (key0 + kKeysPerTile <= kend) {
 #pragma unroll
-            for (int i = 0; i < NF; i++)
+                for (int i = 0; i < T::NI; i++) {
+                    const int inst = wr * T::NI + i;
+                    lds_dma_b128(kb, gk[i], lds_addr(&lds[buf][par][0][inst * 1024]));
+                    lds_dma_b128(vb, gv[i], lds_addr(&lds[buf][par][1][inst * 1024]));
+                }
+            } else {  // last tile: rows past kend (never read unmasked) clamp to kend - 1
+                const int rmax = kend - 1 - key0;
 #pragma unroll
-                for (int e = 0; e < 4; e++) ss = fmaf(x[i][e], x[i][e], ss);
-            ss = group_sum<4>(ss);  // the row's four lanes
-            const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
-#pragma unroll
-            for (int i = 0; i < NF; i++) {
-                const float4 wv = *(const float4*)(s_qw + 4 * pchunk(i));
-                x[i][0] = rms_apply(x[i][0], sc, wv.x);
-                x[i][1] = rms_apply(x[i][1], sc, wv.y);
-                x[i][2] = rms_apply(x[i][2], sc, wv.z);
-                x[i][3] = rms_apply(x[i][3], sc, wv.w);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < NH4; q++) {
-            const float cv[4] = {cf[q].x, cf[q].y, cf[q].z, cf[q].w};
-            const float sv[4] = {sf[q].x, sf[q].y, sf[q].z, sf[q].w};
-            if (a.rope == 0) {  // NeoX: float4 q of half 0 with float4 q of half 1
-#pragma unroll
-                for (int e = 0; e < 4; e++) rope_rotate(x[q][e], x[NH4 + q][e], cv[e], sv[e]);
-            } else {
-                const int i0 = (q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2));  // chunk pair (i0, i0 + 1)
-                if (a.rope == 1) {  // block8: element e of the two halves of the 8-dim chunk
-#pragma unroll
-                    for (int e = 0; e < 4; e++) rope_rotate(x[i0][e], x[i0 + 1][e], cv[e], sv[e]);
-                } else {  // interleaved: (2i, 2i+1), angles 2c .. 2c+3 over the chunk pair
-                    rope_rotate(x[i0][0], x[i0][1], cv[0], sv[0]);
-                    rope_rotate(x[i0][2], x[i0][3], cv[1], sv[1]);
-                    rope_rotate(x[i0 + 1][0], x[i0 + 1][1], cv[2], sv[2]);
-                    rope_rotate(x[i0 + 1][2], x[i0 + 1][3], cv[3], sv[3]);
+                for (int i = 0; i < T::NI; i++) {
+                    const int inst = wr * T::NI + i;
+                    const int r = inst * T::RPI + lane / T::CH;
+                    const int p = lane % T::CH;
+                    const unsigned row = (unsigned)(min(r, rmax) * rowb);
+                    lds_dma_b128(kb, row + 16u * (p ^ T::swz_k(r)), lds_addr(&lds[buf][par][0][inst * 1024]));
+                    lds_dma_b128(vb, row + 16u * (p ^ T::swz_v(r)), lds_addr(&lds[buf][par][1][inst * 1024]));
                 }
             }
+        };
+
+        issue(0, 0);
+
+        // ---- q: normed, rotated, scaled, fp16, into LDS (sq) ----
+        // The q rows of the row group reach LDS (buffer 1, free until the loop)
+        // by direct loads, whole rows per lane group: coalesced, unlike
+        // fragment-shaped loads. Row r's 16-byte chunk c sits at slot c ^ (r mod
+        // chunks per row), so both the reads below and the fragment reads of the
+        // loop are conflict-free. The two waves of a row group prepare 16 rows
+        // each: lane (rr, j) = (lane / 4, lane % 4) holds of row 16 par + rr the
+        // dims j HD/8 .. +HD/8 of both halves, i.e. whole RoPE pairs of all three
+        // pairings (NeoX d ~ d + HD/2; block8 and interleaved inside 8-dim
+        // chunks), so the rotation stays in the lane and the norm is a quad sum.
+        // Until sq is written the same space holds the norm weights.
+        float* s_qw = (float*)&sq[0][0];
+        if (w == 0 && lane < HD / 4)
+            lds_dma_b128(a.qn ? a.qn : a.wpad, 16u * lane, lds_addr(s_qw));
+        constexpr int CQ = HD / 4;            // 16-byte chunks per fp32 q row
+        constexpr int RPQ = 1024 / (HD * 4);  // rows per 1 KB wave load
+        constexpr int NQ = 32 / RPQ / 2;      // loads per wave (the two waves of a row group split them)
+        char* qst = &lds[1][0][0][0] + wr * 32 * HD * 4;
+        const int tq0 = min(R0, a.rows - 1) / a.g;  // first token of the row group
+        const char* qbase = (const char*)(a.q + (size_t)tq0 * a.nh * HD);
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const int j = par * NQ + i;
+            const int rr = j * RPQ + lane / CQ;
+            const int Rq = min(R0 + rr, a.rows - 1);
+            const int tq = Rq / a.g;
+            const unsigned qoff = (unsigned)((((tq - tq0) * a.nh + kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
+            const int c = (lane % CQ) ^ (rr & (CQ - 1));
+            lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
         }
-        const float qs = pR < a.rows ? a.qscale : 0.0f;
-        __syncthreads();  // every wave is done with the norm weights in sq
-        // fp16 chunk (i0 / 2) = float4s (i0, i0 + 1); hi to sq, the residual
-        // (split-q) over the row's own fp32 staging
+        constexpr int NF = HD / 16;       // float4s per lane: NF/2 in each half
+        constexpr int NH4 = NF / 2;       // float4s per half
+        const int prow = 16 * par + (lane >> 2), pj = lane & 3;
+        const int pR = R0 + prow;
+        const int pqpos = a.start + min(pR, a.rows - 1) / a.g;
+        auto pchunk = [&](int i) { return (i / NH4) * (CQ / 2) + pj * NH4 + (i % NH4); };  // fp32 chunk of float4 i
+        half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode, in the MFMA operand layout
+        {
+            // cos/sin float4 q: NeoX the angles of half-0 float4 q (4 * its chunk);
+            // block8 / interleaved the four angles 2c .. 2c+3 of chunk pair (c, c+1)
+            const float* crow = a.cos_tab + (size_t)pqpos * (HD / 2);
+            const float* srow = a.sin_tab + (size_t)pqpos * (HD / 2);
+            float4 cf[NH4], sf[NH4];
 #pragma unroll
-        for (int i0 = 0; i0 < NF; i0 += 2) {
-            half8 hi8, lo8;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float xs = x[i0 + e / 4][e % 4] * qs;
-                hi8[e] = (_Float16)xs;
-                lo8[e] = (_Float16)(xs - (float)hi8[e]);
+            for (int q = 0; q < NH4; q++) {
+                const int ai = a.rope == 0 ? 4 * pchunk(q) : 2 * pchunk((q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2)));
+                cf[q] = *(const float4*)(crow + ai);
+                sf[q] = *(const float4*)(srow + ai);
             }
-            const int slot = 16 * ((pchunk(i0) / 2) ^ (prow & (T::CH - 1)));
-            *(half8*)(sq[wr] + prow * HD * 2 + slot) = hi8;
-            if constexpr (SPLITQ) *(half8*)(qst + prow * HD * 4 + slot) = lo8;
-        }
-        if constexpr (SPLITQ) {
-            __syncthreads();  // both waves' residual rows landed
-            const char* lrow = qst + col * HD * 4;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // q rows and s_qw landed
+            float x[NF][4];
+            const char* rowp = qst + prow * HD * 4;
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++)
-                qfl[ks] = *(const half8*)(lrow + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1))));
-        }
-    }
-    const char* sq_row = sq[wr] + col * HD * 2;
-    auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
-
-    // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
-    // a row whose keys in a tile are all masked (the odd group's first tile
-    // can be) then gets p = exp2(-inf) = 0 and a rescale factor of 1, never
-    // exp2(-inf - -inf).
-    float m_run = -1e30f, l_run = 0.0f;
-    floatx16 o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
-
-    auto tile = [&](int step, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
-        const int kt = 2 * step + par;
-        const int key0 = kt * kKeysPerTile;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of step `step`
-        __syncthreads();                                   // everyone's; the other buffer is free
-        issue(step + 1, buf ^ 1);
-        if (kt >= ntiles || key0 >= kend_w) return;  // wave-uniform: nothing left for this wave
-
-        const char* kt_lds = lds[buf][par][0];
-        const char* vt_lds = lds[buf][par][1];
-        // S^T = K Q^T: k-step ks takes q(ks) and the K fragments of both 32-key
-        // halves; operands come from LDS through a ring RS steps deep, so the
-        // reads run ahead of the MFMAs that consume them.
-        constexpr int RS = 3;
-        floatx16 sacc[2];
-        half8 rq[RS], rk0[RS], rk1[RS];
-#pragma unroll
-        for (int i = 0; i < RS; i++) {
-            rq[i] = qread(i);
-            rk0[i] = *(const half8*)(kt_lds + koff[i]);
-            rk1[i] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[i]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < QK; ks++) {
-            const int sl = ks % RS;
-            const half8 qv = rq[sl], k0 = rk0[sl], k1 = rk1[sl];
-            if (ks + RS < QK) {
-                rq[sl] = qread(ks + RS);
-                rk0[sl] = *(const half8*)(kt_lds + koff[ks + RS]);
-                rk1[sl] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[ks + RS]);
+            for (int i = 0; i < NF; i++) {
+                const float4 u = *(const float4*)(rowp + 16 * (pchunk(i) ^ (prow & (CQ - 1))));
+                x[i][0] = u.x, x[i][1] = u.y, x[i][2] = u.z, x[i][3] = u.w;
             }
-            // keep the reads ahead: the scheduler would otherwise sink them
-            // next to their MFMAs and expose the LDS latency again
-            __builtin_amdgcn_sched_barrier(0);
-            if (ks == 0) {
-                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, floatx16{}, 0, 0, 0);
-                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, floatx16{}, 0, 0, 0);
-            } else {
-                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, sacc[0], 0, 0, 0);
-                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, sacc[1], 0, 0, 0);
+            if (a.qn) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NF; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ss = fmaf(x[i][e], x[i][e], ss);
+                ss = group_sum<4>(ss);  // the row's four lanes
+                const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+#pragma unroll
+                for (int i = 0; i < NF; i++) {
+                    const float4 wv = *(const float4*)(s_qw + 4 * pchunk(i));
+                    x[i][0] = rms_apply(x[i][0], sc, wv.x);
+                    x[i][1] = rms_apply(x[i][1], sc, wv.y);
+                    x[i][2] = rms_apply(x[i][2], sc, wv.z);
+                    x[i][3] = rms_apply(x[i][3], sc, wv.w);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < NH4; q++) {
+                const float cv[4] = {cf[q].x, cf[q].y, cf[q].z, cf[q].w};
+                const float sv[4] = {sf[q].x, sf[q].y, sf[q].z, sf[q].w};
+                if (a.rope == 0) {  // NeoX: float4 q of half 0 with float4 q of half 1
+#pragma unroll
+                    for (int e = 0; e < 4; e++) rope_rotate(x[q][e], x[NH4 + q][e], cv[e], sv[e]);
+                } else {
+                    const int i0 = (q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2));  // chunk pair (i0, i0 + 1)
+                    if (a.rope == 1) {  // block8: element e of the two halves of the 8-dim chunk
+#pragma unroll
+                        for (int e = 0; e < 4; e++) rope_rotate(x[i0][e], x[i0 + 1][e], cv[e], sv[e]);
+                    } else {  // interleaved: (2i, 2i+1), angles 2c .. 2c+3 over the chunk pair
+                        rope_rotate(x[i0][0], x[i0][1], cv[0], sv[0]);
+                        rope_rotate(x[i0][2], x[i0][3], cv[1], sv[1]);
+                        rope_rotate(x[i0 + 1][0], x[i0 + 1][1], cv[2], sv[2]);
+                        rope_rotate(x[i0 + 1][2], x[i0 + 1][3], cv[3], sv[3]);
+                    }
+                }
+            }
+            const float qs = pR < a.rows ? a.qscale : 0.0f;
+            __syncthreads();  // every wave is done with the norm weights in sq
+            // fp16 chunk (i0 / 2) = float4s (i0, i0 + 1); hi to sq, the residual
+            // (split-q) over the row's own fp32 staging
+#pragma unroll
+            for (int i0 = 0; i0 < NF; i0 += 2) {
+                half8 hi8, lo8;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float xs = x[i0 + e / 4][e % 4] * qs;
+                    hi8[e] = (_Float16)xs;
+                    lo8[e] = (_Float16)(xs - (float)hi8[e]);
+                }
+                const int slot = 16 * ((pchunk(i0) / 2) ^ (prow & (T::CH - 1)));
+                *(half8*)(sq[wr] + prow * HD * 2 + slot) = hi8;
+                if constexpr (SPLITQ) *(half8*)(qst + prow * HD * 4 + slot) = lo8;
             }
             if constexpr (SPLITQ) {
-                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qfl[ks], sacc[0], 0, 0, 0);
-                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qfl[ks], sacc[1], 0, 0, 0);
+                __syncthreads();  // both waves' residual rows landed
+                const char* lrow = qst + col * HD * 4;
+#pragma unroll
+                for (int ks = 0; ks < QK; ks++)
+                    qfl[ks] = *(const half8*)(lrow + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1))));
             }
         }
-        // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
-        if (key0 + kKeysPerTile - 1 > qpos_min_w) {
+        const char* sq_row = sq[wr] + col * HD * 2;
+        auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
+
+        // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
+        // a row whose keys in a tile are all masked (the odd group's first tile
+        // can be) then gets p = exp2(-inf) = 0 and a rescale factor of 1, never
+        // exp2(-inf - -inf).
+        float m_run = -1e30f, l_run = 0.0f;
+        floatx16 o[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+
+        auto tile = [&](int step, auto BUF) {
+            constexpr int buf = decltype(BUF)::value;
+            const int kt = 2 * step + par;
+            const int key0 = kt * kKeysPerTile;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of step `step`
+            __syncthreads();                                   // everyone's; the other buffer is free
+            issue(step + 1, buf ^ 1);
+            if (kt >= ntiles || key0 >= kend_w) return;  // wave-uniform: nothing left for this wave
+
+            const char* kt_lds = lds[buf][par][0];
+            const char* vt_lds = lds[buf][par][1];
+            // S^T = K Q^T: k-step ks takes q(ks) and the K fragments of both 32-key
+            // halves; operands come from LDS through a ring RS steps deep, so the
+            // reads run ahead of the MFMAs that consume them.
+            constexpr int RS = 3;
+            floatx16 sacc[2];
+            half8 rq[RS], rk0[RS], rk1[RS];
+#pragma unroll
+            for (int i = 0; i < RS; i++) {
+                rq[i] = qread(i);
+                rk0[i] = *(const half8*)(kt_lds + koff[i]);
+                rk1[i] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < QK; ks++) {
+                const int sl = ks % RS;
+                const half8 qv = rq[sl], k0 = rk0[sl], k1 = rk1[sl];
+                if (ks + RS < QK) {
+                    rq[sl] = qread(ks + RS);
+                    rk0[sl] = *(const half8*)(kt_lds + koff[ks + RS]);
+                    rk1[sl] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[ks + RS]);
+                }
+                // keep the reads ahead: the scheduler would otherwise sink them
+                // next to their MFMAs and expose the LDS latency again
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks == 0) {
+                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, floatx16{}, 0, 0, 0);
+                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, floatx16{}, 0, 0, 0);
+                } else {
+                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, sacc[0], 0, 0, 0);
+                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, sacc[1], 0, 0, 0);
+                }
+                if constexpr (SPLITQ) {
+                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qfl[ks], sacc[0], 0, 0, 0);
+                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qfl[ks], sacc[1], 0, 0, 0);
+                }
+            }
+            // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
+            if (key0 + kKeysPerTile - 1 > qpos_min_w) {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
+                        if (key > qpos) sacc[t2][r] = NEG_INF;
+                    }
+            }
+            float mx = NEG_INF;
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
-                    if (key > qpos) sacc[t2][r] = NEG_INF;
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
+            mx = max_x32(mx);
+            if (__any(mx > m_run + kRescaleSlack)) {
+                const float m_new = fmaxf(m_run, mx);
+                const float corr = fast_exp2(m_run - m_new);
+                m_run = m_new;
+                l_run *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+            }
+            half8 pf[4];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)fast_exp2(sacc[t2][r] - m_run);
+            // row sum of the fp16 P the PV product consumes (v_dot2_f32_f16 with ones)
+            const half2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+            float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    ps[s] = __builtin_amdgcn_fdot2(half2{pf[s][2 * e], pf[s][2 * e + 1]}, one2, ps[s], false);
+            l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+            // O^T += V^T P^T: 4 key steps x DT dim tiles; V^T fragments (two
+            // transposing reads each) through a ring RV MFMAs deep.
+            constexpr int NPV = 4 * DT, RV = 4;
+            auto vread = [&](int idx) {
+                const int s = idx / DT, dt = idx % DT;
+                half4 part[2];
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const char* adr = vt_lds + voff[dt] + (16 * s + 8 * t) * T::ROWB;
+                    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)adr);
+                    part[t] = __builtin_bit_cast(half4, raw);
                 }
+                return half8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
+            };
+            half8 rv[RV];
+#pragma unroll
+            for (int i = 0; i < RV; i++) rv[i] = vread(i);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int idx = 0; idx < NPV; idx++) {
+                const half8 vf = rv[idx % RV];
+                if (idx + RV < NPV) rv[idx % RV] = vread(idx + RV);
+                __builtin_amdgcn_sched_barrier(0);
+                o[idx % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[idx / DT], o[idx % DT], 0, 0, 0);
+            }
+        };
+
+        const int nsteps = (ntiles + 1) / 2;
+        for (int step = 0; step < nsteps; step += 2) {
+            tile(step, std::integral_constant<int, 0>{});
+            if (step + 1 < nsteps) tile(step + 1, std::integral_constant<int, 1>{});
         }
-        float mx = NEG_INF;
-#pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
-        mx = max_x32(mx);
-        if (__any(mx > m_run + kRescaleSlack)) {
-            const float m_new = fmaxf(m_run, mx);
-            const float corr = fast_exp2(m_run - m_new);
-            m_run = m_new;
-            l_run *= corr;
+
+        // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
+        // LDS: [wr][MR][64 lanes] floats: o (16 DT per lane), m, l.
+        constexpr int MR = 16 * DT + 2;
+        static_assert(kGroupWaves * MR * 64 * 4 <= (int)sizeof(lds), "merge area exceeds the tile buffers");
+        __syncthreads();  // tile buffers are free
+        float* mg = (float*)&lds[0][0][0][0] + wr * MR * 64;
+        if (par == 1) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+                for (int r = 0; r < 16; r++) mg[(16 * dt + r) * 64 + lane] = o[dt][r];
+            mg[(MR - 2) * 64 + lane] = m_run;
+            mg[(MR - 1) * 64 + lane] = l_run;
         }
-        half8 pf[4];
+        __syncthreads();
+        if (par == 0) {
+            {
+                const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
+                const float M = fmaxf(m_run, mo);
+                const float fe = fast_exp2(m_run - M);
+                const float fo = fast_exp2(mo - M);
+                l_run = l_run * fe + lo * fo;
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
+                for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)fast_exp2(sacc[t2][r] - m_run);
-        // row sum of the fp16 P the PV product consumes (v_dot2_f32_f16 with ones)
-        const half2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                ps[s] = __builtin_amdgcn_fdot2(half2{pf[s][2 * e], pf[s][2 * e + 1]}, one2, ps[s], false);
-        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-        // O^T += V^T P^T: 4 key steps x DT dim tiles; V^T fragments (two
-        // transposing reads each) through a ring RV MFMAs deep.
-        constexpr int NPV = 4 * DT, RV = 4;
-        auto vread = [&](int idx) {
-            const int s = idx / DT, dt = idx % DT;
-            half4 part[2];
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const char* adr = vt_lds + voff[dt] + (16 * s + 8 * t) * T::ROWB;
-                const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)adr);
-                part[t] = __builtin_bit_cast(half4, raw);
+                    for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * fe + mg[(16 * dt + r) * 64 + lane] * fo;
             }
-            return half8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
-        };
-        half8 rv[RV];
+
+            // ---- normalise and store ----
+            // The wave's 32 rows go through its own merge area (read above; LDS
+            // operations of one wave run in order) as [row][HD] fp32, 16-byte chunk c
+            // of row r at slot c ^ (r mod chunks), so that each store instruction
+            // writes whole 512-byte output rows instead of 32-byte pieces of 32 rows.
+            constexpr int CPR = HD / 4;  // 16-byte chunks per output row
+            static_assert(32 * HD <= MR * 64, "output staging exceeds the merge area");
+            const float inv = 1.0f / sum_x32(l_run);
+            const int orow = rvalid ? tok * a.nh + hq : -1;  // output row of q row `col`
+            wave_sync();
 #pragma unroll
-        for (int i = 0; i < RV; i++) rv[i] = vread(i);
-        __builtin_amdgcn_sched_barrier(0);
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-        for (int idx = 0; idx < NPV; idx++) {
-            const half8 vf = rv[idx % RV];
-            if (idx + RV < NPV) rv[idx % RV] = vread(idx + RV);
-            __builtin_amdgcn_sched_barrier(0);
-            o[idx % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[idx / DT], o[idx % DT], 0, 0, 0);
+                for (int r4 = 0; r4 < 4; r4++) {
+                    const int c = 8 * dt + 2 * r4 + hk;  // dims 32 dt + 8 r4 + 4 hk .. +3
+                    *(floatx4*)(mg + col * HD + 4 * (c ^ (col & (CPR - 1)))) =
+                        floatx4{o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                                o[dt][4 * r4 + 3] * inv};
+                }
+            wave_sync();
+#pragma unroll
+            for (int i = 0; i < 32 * CPR / 64; i++) {
+                constexpr int RPS = 64 / CPR;  // rows per store instruction
+                const int rr = RPS * i + lane / CPR, c = lane % CPR;
+                int orr = -1;
+#pragma unroll
+                for (int u = 0; u < RPS; u++) {
+                    const int v = __builtin_amdgcn_readlane(orow, RPS * i + u);
+                    if (lane / CPR == u) orr = v;
+                }
+                const floatx4 vv = *(const floatx4*)(mg + rr * HD + 4 * (c ^ (rr & (CPR - 1))));
+                if (orr >= 0) *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv;
+            }
         }
-    };
-
-    const int nsteps = (ntiles + 1) / 2;
-    for (int step = 0; step < nsteps; step += 2) {
-        tile(step, std::integral_constant<int, 0>{});
-        if (step + 1 < nsteps) tile(step + 1, std::integral_constant<int, 1>{});
-    }
-
-    // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
-    // LDS: [wr][MR][64 lanes] floats: o (16 DT per lane), m, l.
-    constexpr int MR = 16 * DT + 2;
-    static_assert(kGroupWaves * MR * 64 * 4 <= (int)sizeof(lds), "merge area exceeds the tile buffers");
-    __syncthreads();  // tile buffers are free
-    float* mg = (float*)&lds[0][0][0][0] + wr * MR * 64;
-    if (par == 1) {
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) mg[(16 * dt + r) * 64 + lane] = o[dt][r];
-        mg[(MR - 2) * 64 + lane] = m_run;
-        mg[(MR - 1) * 64 + lane] = l_run;
-    }
-    __syncthreads();
-    if (par == 1) return;
-    {
-        const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
-        const float M = fmaxf(m_run, mo);
-        const float fe = fast_exp2(m_run - M);
-        const float fo = fast_exp2(mo - M);
-        l_run = l_run * fe + lo * fo;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * fe + mg[(16 * dt + r) * 64 + lane] * fo;
-    }
-
-    const float l_tot = sum_x32(l_run);
-    if (rvalid) {
-        const float inv = 1.0f / l_tot;
-        float* op = a.out + ((size_t)tok * a.nh + hq) * HD + 4 * hk;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                floatx4 vv = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
-                              o[dt][4 * r4 + 3] * inv};
-                *(floatx4*)(op + 32 * dt + 8 * r4) = vv;
-            }
     }
 }
 
@@ -572,7 +610,7 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     a.nblk = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
     a.rope = ctx->rope_style;
     a.qscale = 1.4426950408889634f / sqrtf((float)HD);
-    dim3 grid(a.nblk * ctx->n_kv_heads);
+    dim3 grid((a.nblk + 1) / 2 * ctx->n_kv_heads);  // pairs of row blocks
     if (ctx->prefill_split_q)
         hipLaunchKernelGGL((prefill_attn_kernel<HD, true>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     else
