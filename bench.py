@@ -15,6 +15,7 @@ Also reported in the same JSON line under "workloads":
   tinyllama_decode    32/4/64, block8 RoPE, pos 511, 1 layer (latency)
   qwen2.5_0.5b_sweep  14/2/64, positions 0..4095 token by token, 24 layers
   qwen3_8b_kvc_save_load  .kvc save/load of 4096 positions x 36 layers (604 MB)
+  qwen3_8b_qkv_proj   Q/K/V projections of one token, Q4_K/Q4_K/Q6_K, 36 layers
 
 `roofline` covers the decode kernel of the headline workload, timed with HIP
 events on the library's stream. `cpu_baseline` times the CPU oracle (the
@@ -283,6 +284,77 @@ def kvc_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n_pos=4096, reps
     return res
 
 
+def gguf_rows(rng, wtype, rows, n):
+    """Synthetic GGUF rows: random payload, fp16 scale fields of a realistic size."""
+    be, bb, scales = {13: (256, 144, (0, 2)), 15: (256, 210, (208,))}[wtype]
+    nb = n // be
+    raw = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+    for off in scales:
+        raw[:, :, off:off + 2] = rng.uniform(1e-3, 2e-2, (rows, nb)).astype("<f2").view(np.uint8).reshape(rows, nb, 2)
+    return raw.reshape(rows, nb * bb)
+
+
+def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=20, warmup=3, cpu=True):
+    """Q/K/V projections of one token (matmul_bias, cpp/model.hpp:320-366) for a
+    Qwen3-8B-shaped layer stored as a Q4_K_M file stores it: Q4_K attn_q and
+    attn_k, Q6_K attn_v, 4096-wide rows; 36 layers rotated per step (547 MB of
+    weights, more than the Infinity Cache). Unit: weight GB/s."""
+    Q4K, Q6K = 13, 15
+    cx = Ctx(n_layers, 64, nh, nkv, hd, 0, 1e6)
+    rng = np.random.default_rng(606)
+    wbytes = 0
+    for layer in range(n_layers):
+        wq, wk, wv = gguf_rows(rng, Q4K, nh * hd, n), gguf_rows(rng, Q4K, nkv * hd, n), gguf_rows(rng, Q6K, nkv * hd, n)
+        if layer == 0:
+            w0 = (wq, wk, wv)
+            wbytes = wq.nbytes + wk.nbytes + wv.nbytes
+        vp = lambda a: a.ctypes.data_as(C.c_void_p)
+        cx.check(cx.L.pqa_set_qkv_weights(cx.h, layer, n, vp(wq), Q4K, None, 0, vp(wk), Q4K, None, 0, vp(wv), Q6K,
+                                          None, 0), cx.h)
+    x = torch.from_numpy(rng.standard_normal((n_layers, n), dtype=np.float32)).to(dev)
+    q = torch.empty((n_layers, nh * hd), device=dev)
+    k = torch.empty((n_layers, nkv * hd), device=dev)
+    v = torch.empty((n_layers, nkv * hd), device=dev)
+    torch.cuda.synchronize()
+    proj = cx.L.pqa_qkv_project
+    ptrs = [(C.c_void_p(x[l].data_ptr()), C.c_void_p(q[l].data_ptr()), C.c_void_p(k[l].data_ptr()),
+             C.c_void_p(v[l].data_ptr())) for l in range(n_layers)]
+
+    def step():
+        for layer in range(n_layers):
+            proj(cx.h, layer, *ptrs[layer])
+
+    wall, ev = timed(torch, cx, step, steps, warmup)
+    us = ev * 1e3 / n_layers
+    gbs = wbytes / (us * 1e-6) / 1e9
+    res = {"workload": "qwen3_8b_qkv_proj_q4_k_m", "n_embd": n, "rows": [nh * hd, nkv * hd, nkv * hd],
+           "weight_types": ["Q4_K", "Q4_K", "Q6_K"], "weight_bytes_per_layer": wbytes,
+           "us_per_layer": round(us, 3), "weight_GB_per_s": round(gbs, 1),
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bit_exact_vs_reference_build_B": True}
+    if cpu:
+        import oracle as O
+        if O.RefModel.available("B"):
+            ref = O.RefProj("B")
+            xh = x[0].cpu().numpy()
+            reps, total = 0, 0.0
+            while total < 6.0 and reps < 50:
+                t0 = time.perf_counter()
+                for w, wt in zip(w0, (Q4K, Q4K, Q6K)):
+                    ref.matmul_bias(xh, w, wt, w.shape[0])
+                total += time.perf_counter() - t0
+                reps += 1
+            per = total / reps
+            res["cpu_baseline"] = {"kind": "reference", "cores": 1, "us_per_layer": round(per * 1e6, 1),
+                                   "weight_GB_per_s": round(wbytes / per / 1e9, 3),
+                                   "sample": f"TensorOps::matmul_bias of the reference (build B) on layer 0, {reps}x"}
+            qg = q[0].cpu().numpy()
+            res["q_layer0_bit_exact"] = bool(np.array_equal(qg.view(np.uint32),
+                                                            ref.matmul_bias(xh, w0[0], Q4K, nh * hd).view(np.uint32)))
+    cx.close()
+    log(f"[bench] qkv projection: {us:.2f} us/layer, {gbs:.0f} GB/s of weights ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); {res.get('cpu_baseline')}")
+    return res
+
+
 def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
     """The oracle (reference attention loop, restated in C) on layer 0 of the
     headline cache: same K/V bytes (downloaded), same q/k/v and norm weights."""
@@ -435,7 +507,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
     ap.add_argument("--only", choices=["qwen3_1.7b_decode", "qwen3_4b_prefill", "tinyllama_decode",
-                                       "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load"],
+                                       "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load", "qwen3_8b_qkv_proj"],
                     help="run one secondary workload and print it")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
@@ -468,6 +540,7 @@ def main():
                                                         0.0, max(args.steps, 200), args.warmup, False)[0],
             "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev),
             "qwen3_8b_kvc_save_load": lambda: kvc_workload(torch, dev),
+            "qwen3_8b_qkv_proj": lambda: proj_workload(torch, dev, steps=args.steps, warmup=args.warmup),
         }
         print(json.dumps({args.only: runs[args.only]()}), flush=True)
         return
@@ -492,6 +565,8 @@ def main():
                                                         0.0, max(args.steps, 200), args.warmup, False)[0]
         workloads["qwen2.5_0.5b_sweep"] = sweep_workload(torch, dev)
         workloads["qwen3_8b_kvc_save_load"] = kvc_workload(torch, dev)
+        workloads["qwen3_8b_qkv_proj"] = proj_workload(torch, dev, steps=args.steps, warmup=args.warmup,
+                                                       cpu=not args.no_cpu)
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]

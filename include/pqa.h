@@ -136,6 +136,48 @@ int pqa_kvc_save(pqa_ctx* ctx, const char* path, int n_pos);
  */
 int pqa_kvc_load(pqa_ctx* ctx, const char* path);
 
+/*
+ * Q/K/V projections of the decode step: TensorOps::matmul_bias
+ * (cpp/tensor.hpp:110-143) for ATTN_Q, ATTN_K and ATTN_V as Model::forward
+ * calls it (cpp/model.hpp:320-366), on the GPU and in the reference's own
+ * summation order (the x86 SSE2 path of vec_dot, cpp/quant.hpp:297-356), so
+ * q, k and v are bit-identical to the reference built without FMA contraction.
+ *
+ * Weight and bias types are the reference's GGUFType numbers
+ * (cpp/quant.hpp:16-31), as the caller holds them in its tensor entries.
+ */
+#define PQA_GGUF_NONE 0
+#define PQA_GGUF_F32 1
+#define PQA_GGUF_F16 2
+#define PQA_GGUF_Q4_0 3
+#define PQA_GGUF_Q8_0 9
+#define PQA_GGUF_Q4_K 13
+#define PQA_GGUF_Q6_K 15
+
+/* Uploads one layer's attn_q/attn_k/attn_v weights: HOST pointers to GGUF
+ * rows, [q_dim][row] for wq and [kv_dim][row] for wk/wv, row = n_embd
+ * elements in the type's blocks (the tensor data as the reference maps it).
+ * Biases: HOST [rows] in F32 or F16, or NULL / PQA_GGUF_NONE for none
+ * (the attn_*_b entries). Types: F32, F16, Q4_0, Q8_0, Q4_K, Q6_K;
+ * PQA_ERR_UNSUPPORTED for other types, n_embd > 8192, rows that are not
+ * whole blocks, F32/F16 rows not a multiple of 8, Q4_0/Q8_0 rows not a
+ * multiple of 64 or Q6_K rows not a multiple of 512 elements. Synchronous;
+ * replaces earlier weights of the layer. */
+int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wq, int wq_type, const void* bq,
+                        int bq_type, const void* wk, int wk_type, const void* bk, int bk_type, const void* wv,
+                        int wv_type, const void* bv, int bv_type);
+
+/* q = Wq xb + bq, k = Wk xb + bk, v = Wv xb + bv for one token (the
+ * matmul_bias calls of cpp/model.hpp:320-323, :337-340, :362-365). DEVICE
+ * pointers xb [n_embd], q [n_heads*head_dim], k and v [n_kv_heads*head_dim];
+ * asynchronous on the context stream. */
+int pqa_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);
+
+/* The attention block of Model::forward from the normed input on
+ * (cpp/model.hpp:320-418): pqa_qkv_project into a context workspace, then
+ * pqa_decode. DEVICE pointers xb [n_embd], out [n_heads*head_dim]. */
+int pqa_decode_x(pqa_ctx* ctx, int layer, int pos, const float* xb, float* out);
+
 /* The context's HIP stream (a hipStream_t), for event timing or ordering. */
 void* pqa_stream(pqa_ctx* ctx);
 int pqa_sync(pqa_ctx* ctx);

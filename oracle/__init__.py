@@ -76,6 +76,12 @@ def lib():
     L.pqo_is_outlier.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64, C.c_float]
     L.pqo_synth_kv_rows.argtypes = [C.c_uint64, C.c_uint32, C.c_int, C.c_int, C.c_int, C.c_float,
                                     _u16p, _u16p, C.c_int]
+    L.pqo_row_bytes.restype = C.c_size_t
+    L.pqo_row_bytes.argtypes = [C.c_int, C.c_int]
+    L.pqo_dequant_row.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_int]
+    L.pqo_vec_dot.restype = C.c_float
+    L.pqo_vec_dot.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_int]
+    L.pqo_matmul_bias.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]
     _lib = L
     return L
 
@@ -242,6 +248,43 @@ def qk_norm_weights(seed, layer, head_dim):
             normal(seed, KIND_KNORM, layer, 0, head_dim, 1.0, 0.02))
 
 
+# ---- Q/K/V projections (cpp/tensor.hpp:110-143, cpp/quant.hpp:176-358) ---------
+
+GGUF_NONE, GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q8_0, GGUF_Q4_K, GGUF_Q6_K = 0, 1, 2, 3, 9, 13, 15
+GGUF_BLOCK = {GGUF_F32: (1, 4), GGUF_F16: (1, 2), GGUF_Q4_0: (32, 18), GGUF_Q8_0: (32, 34),
+              GGUF_Q4_K: (256, 144), GGUF_Q6_K: (256, 210)}  # (elements, bytes) per block
+
+
+def row_bytes(wtype, n):
+    return int(lib().pqo_row_bytes(wtype, n))
+
+
+def _vp(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def dequant_row(wtype, raw, n):
+    out = np.empty(n, np.float32)
+    if lib().pqo_dequant_row(wtype, _vp(np.ascontiguousarray(raw)), out, n):
+        raise ValueError("unsupported type or shape")
+    return out
+
+
+def vec_dot(wtype, raw_row, x):
+    x = np.ascontiguousarray(x, np.float32)
+    return float(lib().pqo_vec_dot(wtype, _vp(np.ascontiguousarray(raw_row)), x, x.size))
+
+
+def matmul_bias(x, w_raw, wtype, d, b_raw=None, btype=GGUF_NONE):
+    """out[d] = W x (+ b): w_raw uint8 [d][row_bytes], b_raw uint8 bias row or None."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(d, np.float32)
+    if lib().pqo_matmul_bias(out, x, _vp(np.ascontiguousarray(w_raw)), wtype,
+                             _vp(None if b_raw is None else np.ascontiguousarray(b_raw)), btype, x.size, d):
+        raise ValueError("unsupported type or shape")
+    return out
+
+
 # ---- reference harness (only where it was built) -----------------------------
 
 class RefModel:
@@ -270,6 +313,10 @@ class RefModel:
         L.ref_fp16_to_fp32_all.argtypes = [_f32p]
         L.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int]
         L.ref_rope.argtypes = [C.c_int, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+        L.ref_dequantize_row.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int]
+        L.ref_vec_dot.restype = C.c_float
+        L.ref_vec_dot.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int]
+        L.ref_matmul_bias.argtypes = [_f32p, _f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int]
         cls._libs[variant] = L
         return L
 
@@ -421,3 +468,28 @@ class RefKvc:
         n_layers, max_seq_len, _ = key_cache.shape
         return cls.load().refkvc_load(key_cache, val_cache, n_layers, max_seq_len, n_kv_heads, head_dim,
                                       os.fsencode(path))
+
+
+class RefProj:
+    """The reference's dequantize_row / vec_dot / TensorOps::matmul_bias
+    (oracle/ref_harness.cpp, build B unless stated)."""
+
+    def __init__(self, variant="B"):
+        self.L = RefModel.load(variant)
+
+    def dequant_row(self, wtype, raw, n):
+        out = np.empty(n, np.float32)
+        self.L.ref_dequantize_row(_vp(np.ascontiguousarray(raw)), out, n, wtype)
+        return out
+
+    def vec_dot(self, wtype, raw_row, x):
+        x = np.ascontiguousarray(x, np.float32)
+        return float(self.L.ref_vec_dot(_vp(np.ascontiguousarray(raw_row)), x, x.size, wtype))
+
+    def matmul_bias(self, x, w_raw, wtype, d, b_raw=None, btype=GGUF_NONE):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(d, np.float32)
+        self.L.ref_matmul_bias(out, x, _vp(np.ascontiguousarray(w_raw)),
+                               _vp(None if b_raw is None else np.ascontiguousarray(b_raw)), x.size, d, wtype,
+                               btype if b_raw is not None else GGUF_NONE)
+        return out

@@ -128,6 +128,19 @@ enum {
     PQO_KIND_QNORM = 6, PQO_KIND_KNORM = 7, PQO_KIND_OUTLIER = 8
 };
 
+/* ---- Q/K/V projections (cpp/tensor.hpp:110-143, cpp/quant.hpp:176-358),
+ *      pqa_oracle_proj.c; pinned against the reference's own dequantize_row,
+ *      vec_dot and matmul_bias (tests/test_oracle_proj.py) ---- */
+enum {
+    PQO_GGUF_NONE = 0, PQO_GGUF_F32 = 1, PQO_GGUF_F16 = 2, PQO_GGUF_Q4_0 = 3,
+    PQO_GGUF_Q8_0 = 9, PQO_GGUF_Q4_K = 13, PQO_GGUF_Q6_K = 15
+};  /* the reference's GGUFType numbers (cpp/quant.hpp:16-31) */
+size_t pqo_row_bytes(int type, int n);
+int    pqo_dequant_row(int type, const void* src, float* dst, int n);
+float  pqo_vec_dot(int type, const void* row, const float* x, int n);
+int    pqo_matmul_bias(float* out, const float* x, const void* w, int wtype, const void* b, int btype,
+                       int n, int d);
+
 #ifdef __cplusplus
 }
 #endif

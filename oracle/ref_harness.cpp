@@ -233,4 +233,14 @@ void ref_rope(int qwen, float* q, float* k, int hd, int nh, int nkv, const float
     else TensorOps::rope_llama(q, k, hd, nh, nkv, c, s);
 }
 
+// The projection path of Model::forward as the reference computes it
+// (cpp/model.hpp:320-366): dequantize_row, vec_dot and TensorOps::matmul_bias
+// themselves, for the oracle's projection pins.
+void ref_dequantize_row(const void* src, float* dst, int n, int type) { dequantize_row(src, dst, n, (GGUFType)type); }
+float ref_vec_dot(const void* row, const float* x, int n, int type) { return vec_dot(row, x, n, (GGUFType)type); }
+void ref_matmul_bias(float* out, const float* x, const void* w, const void* b, int n, int d, int wtype, int btype) {
+    std::vector<float> scratch((size_t)d);
+    TensorOps::matmul_bias(out, x, w, b, n, d, (GGUFType)wtype, (GGUFType)btype, scratch.data());
+}
+
 }  // extern "C"

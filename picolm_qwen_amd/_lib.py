@@ -16,11 +16,14 @@ PQA_ERR_NOMEM = -5
 PQA_ERR_IO = -6
 PQA_ERR_FORMAT = -7
 
+GGUF_NONE, GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q8_0, GGUF_Q4_K, GGUF_Q6_K = 0, 1, 2, 3, 9, 13, 15
+
 EXPORTS = [
     "pqa_create", "pqa_set_qk_norm", "pqa_decode", "pqa_prefill", "pqa_decode_host",
     "pqa_prefill_host", "pqa_kv_upload", "pqa_kv_download", "pqa_kv_cache", "pqa_stream",
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
     "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
+    "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x",
 ]
 
 
@@ -66,6 +69,9 @@ def lib() -> C.CDLL:
     L.pqa_set_prefill_precision.argtypes = [vp, i]
     L.pqa_kvc_save.argtypes = [vp, C.c_char_p, i]
     L.pqa_kvc_load.argtypes = [vp, C.c_char_p]
+    L.pqa_set_qkv_weights.argtypes = [vp, i, i] + [vp, i, vp, i] * 3
+    L.pqa_qkv_project.argtypes = [vp, i, vp, vp, vp, vp]
+    L.pqa_decode_x.argtypes = [vp, i, i, vp, vp]
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int

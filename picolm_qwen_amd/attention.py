@@ -220,6 +220,46 @@ class PicoAttention:
         check(lib().pqa_kv_cache(self.handle, C.byref(kp), C.byref(vp)), self.handle)
         return kp.value, vp.value
 
+    # -- Q/K/V projections (cpp/model.hpp:320-366) -----------------------------
+    def set_qkv_weights(self, layer: int, n_embd: int, wq, wq_type: int, wk, wk_type: int, wv, wv_type: int,
+                        bq=None, bq_type: int = 0, bk=None, bk_type: int = 0, bv=None, bv_type: int = 0) -> None:
+        """attn_q/k/v GGUF rows (uint8 arrays, [rows][row bytes]) and optional F32/F16 biases."""
+        keep = []
+
+        def ptr(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+            return a.ctypes.data_as(C.c_void_p)
+        check(lib().pqa_set_qkv_weights(self.handle, layer, n_embd, ptr(wq), wq_type, ptr(bq), bq_type,
+                                        ptr(wk), wk_type, ptr(bk), bk_type, ptr(wv), wv_type, ptr(bv), bv_type),
+              self.handle)
+
+    def qkv_project(self, layer: int, xb, q=None, k=None, v=None):
+        """q, k, v = matmul_bias(xb) on the GPU (torch tensors on the device)."""
+        import torch
+        dev = xb.device
+        q = torch.empty(self.q_dim, dtype=torch.float32, device=dev) if q is None else q
+        k = torch.empty(self.kv_dim, dtype=torch.float32, device=dev) if k is None else k
+        v = torch.empty(self.kv_dim, dtype=torch.float32, device=dev) if v is None else v
+        ext = self._enter(dev, (xb, q, k, v))
+        check(lib().pqa_qkv_project(self.handle, layer, C.c_void_p(xb.data_ptr()), C.c_void_p(q.data_ptr()),
+                                    C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr())), self.handle)
+        self._leave(dev, ext)
+        return q, k, v
+
+    def forward_x(self, layer: int, pos: int, xb, out=None):
+        """The attention block from the normed input xb: projections, then decode at pos."""
+        import torch
+        dev = xb.device
+        out = torch.empty(self.q_dim, dtype=torch.float32, device=dev) if out is None else out
+        ext = self._enter(dev, (xb, out))
+        check(lib().pqa_decode_x(self.handle, layer, pos, C.c_void_p(xb.data_ptr()), C.c_void_p(out.data_ptr())),
+              self.handle)
+        self._leave(dev, ext)
+        return out
+
     # -- .kvc persistence (picolm/model.c:870-983) ---------------------------
     def kvc_save(self, path: str, n_pos: int) -> None:
         """kvcache_save: rows [0, n_pos) of every layer to `path`; raises PQAError."""

@@ -171,6 +171,17 @@ __device__ __forceinline__ void lds_dma_b128(const void* base, unsigned voff, un
                  : "memory", "m0");
 }
 
+// 4 bytes per lane (global_load_lds_dword): lane l's dword lands at LDS byte
+// address lds + 4 l. Same contract as lds_dma_b128.
+__device__ __forceinline__ void lds_dma_b32(const void* base, unsigned voff, unsigned lds) {
+    base = uniform_ptr(base);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
 // ---- cross-lane exchanges without LDS round trips ----
 // DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
 // row_half_mirror (lane ^ 7 within 8), row_mirror (lane ^ 15 within 16),

@@ -8,6 +8,22 @@
 
 #include "pqa.h"
 
+#define PQA_MAX_EMBD 8192  // longest projection input row (x and the chunk rings share the LDS)
+
+namespace pqa {
+// GGUF tensor types as the reference numbers them (cpp/quant.hpp:16-31)
+enum : int { GG_NONE = 0, GG_F32 = 1, GG_F16 = 2, GG_Q4_0 = 3, GG_Q8_0 = 9, GG_Q4_K = 13, GG_Q6_K = 15 };
+}
+
+// One layer's Q, K and V projection weights in HBM: GGUF rows at a 16-byte
+// stride, biases (F32 or F16) or null.
+struct pqa_proj_weights {
+    void* w[3] = {nullptr, nullptr, nullptr};
+    void* b[3] = {nullptr, nullptr, nullptr};
+    int wtype[3] = {0, 0, 0}, btype[3] = {0, 0, 0}, stride[3] = {0, 0, 0};
+    int n_embd = 0;  // 0: not set
+};
+
 struct pqa_ctx {
     int n_layers = 0, max_seq_len = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, rope_style = 0;
     int kv_mul = 1;            // query heads per KV head (cpp/model.hpp:295)
@@ -32,6 +48,10 @@ struct pqa_ctx {
 
     // prefill: q = fp16 hi + lo in the score products (outlier-heavy caches)
     int prefill_split_q = 0;
+
+    // projections (pqa_set_qkv_weights) and the q/k/v of pqa_decode_x
+    std::vector<pqa_proj_weights> proj;
+    float* qkv = nullptr;  // [q_dim + 2 kv_dim]
 
     // staging for the _host entry points
     float* stage = nullptr;
@@ -62,5 +82,9 @@ hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const f
                           const float* k, const float* v, float* out);
 hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
 hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
+hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);
 
 }  // namespace pqa
+
+// Frees every layer's projection weights (pqa_proj.hip).
+void pqa_free_projections(pqa_ctx* c);

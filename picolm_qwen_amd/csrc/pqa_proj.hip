@@ -1,0 +1,479 @@
+// Q/K/V projections of one token on the GPU: TensorOps::matmul_bias
+// (cpp/tensor.hpp:110-143) for ATTN_Q, ATTN_K and ATTN_V at
+// cpp/model.hpp:320-366, in the reference's own summation order, so q, k and
+// v equal the reference's bit for bit (as compiled without FMA contraction)
+// and the K/V rows the decode appends stay bit-exact from xb on.
+//
+// Weights keep the GGUF block layout the reference reads (cpp/quant.hpp:33-63),
+// one row per output element, uploaded once per layer with the row stride
+// rounded up to 16 bytes. Orders reproduced (cpp/quant.hpp:297-356):
+//   F32, F16, Q4_0, Q4_K, Q6_K  row dequantized element by element
+//       (dequantize_row_*, same expressions), then vec_dot_f32_f32's SSE2
+//       order: 8 sequential chains (element i goes to chain i mod 8), then
+//       t = chain l + chain l+4, then (t0 + t2) + (t1 + t3);
+//   Q8_0  per 32-block sequential sums of q*x, then sumf += d * sum in block
+//       order.
+// Then out = out + bias (vec_add), bias F32 or F16.
+//
+// Only the additions are ordered; dequantization and the products w * x are
+// not. A workgroup of 16 waves owns 8 rows: the rows stream in chunks from
+// HBM into a 4-slot LDS ring by direct global->LDS loads (chunk t + 3 in
+// flight while t is used); waves 1-15 turn chunk t into fp32 products
+// round(w * x) in LDS, chain-major (Q8_0: block-major with each block's d),
+// while wave 0, lane 8 r + c, adds chunk t - 1 into chain c of row r. Two
+// barriers per chunk. The work is VALU- and latency-bound by the fixed order
+// (no MFMA or packed math can keep it).
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "pqa_device.h"
+#include "pqa_internal.h"
+
+namespace pqa {
+
+constexpr int kProjWaves = 16;        // wave 0 sums the chains, waves 1-15 produce
+constexpr int kProjProducers = 64 * (kProjWaves - 1);
+constexpr int kProjRows = 8;          // rows per workgroup
+constexpr int kProjChunkMax = 512;    // largest chunk bytes per row
+constexpr int kProjKC = 64;           // largest chain elements per chunk
+constexpr int kPS = kProjKC + 4;      // product row stride (floats): chains off the bank period
+constexpr int kProjSlots = 4;         // raw chunk ring: chunk t + 3 loads while t is used
+constexpr int kProjSlotBytes = kProjRows * kProjChunkMax;  // 16 DMA loads of 256 bytes
+constexpr int kProjDmaPerWave = kProjSlotBytes / 256 / kProjWaves;
+
+struct ProjMat {
+    const uint8_t* w;  // [rows][stride] GGUF rows
+    const uint8_t* b;  // bias row or null
+    float* out;
+    int rows, wtype, btype, stride, wg0;  // wg0: first workgroup of this matrix
+};
+
+struct ProjArgs {
+    ProjMat m[3];
+    const float* x;
+    int n, nmat;
+};
+
+__device__ __forceinline__ float h2f(unsigned h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
+__device__ __forceinline__ unsigned ld16(const uint8_t* p) { return *(const unsigned short*)p; }
+
+// chunk geometry per type: elements and bytes per row, both whole blocks with
+// 4-byte aligned offsets
+template <int T> struct QT;
+template <> struct QT<GG_F32> { static constexpr int CE = 128, CB = 512; };
+template <> struct QT<GG_F16> { static constexpr int CE = 256, CB = 512; };
+template <> struct QT<GG_Q4_0> { static constexpr int CE = 512, CB = 288; };
+template <> struct QT<GG_Q8_0> { static constexpr int CE = 256, CB = 272; };
+template <> struct QT<GG_Q4_K> { static constexpr int CE = 512, CB = 288; };
+template <> struct QT<GG_Q6_K> { static constexpr int CE = 512, CB = 420; };
+
+// get_scale_min_k4 (cpp/quant.hpp:210-218)
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, unsigned& sc, unsigned& mn) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        mn = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// Products of one chunk, round(w * x) in fp32 with w dequantized by the
+// expressions of dequantize_row_* (cpp/quant.hpp:176-281). Chain types:
+// element e of row r at prod[(8 r + e % 8) * kPS + e / 8] (a chain lane reads
+// its products as consecutive floats). Q8_0: q * x of element j of block bi at
+// prod[(8 r + bi) * kPS + j], the block's d at slot 32. Every element of the
+// chunk is written, past the row end too (never summed).
+template <int T>
+__device__ __forceinline__ void produce(const uint8_t* raw, const float* xs, float* prod, int pt) {
+    constexpr int CB = QT<T>::CB, RB = (CB + 3) / 4 * 4;  // LDS bytes per raw row
+    auto put = [&](int r, int e, float v) __attribute__((always_inline)) { prod[(8 * r + (e & 7)) * kPS + (e >> 3)] = v; };
+    if constexpr (T == GG_F32) {  // 8 rows x 32 float4
+        for (int it = pt; it < 8 * 32; it += kProjProducers) {
+            const int r = it >> 5, f = it & 31;
+            const floatx4 v = *(const floatx4*)(raw + r * RB + 16 * f);
+            const floatx4 x = *(const floatx4*)(xs + 4 * f);
+#pragma unroll
+            for (int b = 0; b < 4; b++) put(r, 4 * f + b, v[b] * x[b]);
+        }
+    } else if constexpr (T == GG_F16) {  // 8 rows x 64 groups of 4 halfs
+        for (int it = pt; it < 8 * 64; it += kProjProducers) {
+            const int r = it >> 6, g = it & 63;
+            const u32x2 v = *(const u32x2*)(raw + r * RB + 8 * g);
+            const floatx4 x = *(const floatx4*)(xs + 4 * g);
+            put(r, 4 * g + 0, h2f(v.x & 0xFFFF) * x[0]);
+            put(r, 4 * g + 1, h2f(v.x >> 16) * x[1]);
+            put(r, 4 * g + 2, h2f(v.y & 0xFFFF) * x[2]);
+            put(r, 4 * g + 3, h2f(v.y >> 16) * x[3]);
+        }
+    } else if constexpr (T == GG_Q4_0) {  // 8 rows x 16 blocks x 8 byte pairs: d * ((float)nibble - 8)
+        for (int it = pt; it < 8 * 128; it += kProjProducers) {
+            const int r = it >> 7, bi = (it >> 3) & 15, j2 = 2 * (it & 7);
+            const uint8_t* blk = raw + r * RB + 18 * bi;
+            const float d = h2f(ld16(blk));
+            const unsigned two = ld16(blk + 2 + j2);
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const unsigned byte = (two >> (8 * b)) & 0xFF;
+                const int e = 32 * bi + j2 + b;
+                put(r, e, d * ((float)(byte & 0xF) - 8.0f) * xs[e]);
+                put(r, e + 16, d * ((float)(byte >> 4) - 8.0f) * xs[e + 16]);
+            }
+        }
+    } else if constexpr (T == GG_Q8_0) {  // 8 rows x 8 blocks x 8 groups of 4: (float)q * x
+        for (int it = pt; it < 8 * 64; it += kProjProducers) {
+            const int r = it >> 6, bi = (it >> 3) & 7, g = it & 7;
+            const uint8_t* blk = raw + r * RB + 34 * bi;
+            const unsigned lo = ld16(blk + 2 + 4 * g), hi = ld16(blk + 4 + 4 * g);
+            const unsigned q4 = lo | (hi << 16);
+            float* pr = prod + (8 * r + bi) * kPS;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                pr[4 * g + b] = (float)(int)(int8_t)((q4 >> (8 * b)) & 0xFF) * xs[32 * bi + 4 * g + b];
+            if (g == 0) pr[32] = h2f(ld16(blk));
+        }
+    } else if constexpr (T == GG_Q4_K) {  // 8 rows x 2 blocks x 32 qs dwords: (d * sc) * q - dmin * mn
+        for (int it = pt; it < 8 * 64; it += kProjProducers) {
+            const int r = it >> 6, bk = (it >> 5) & 1, w = it & 31, jj = w >> 3, l0 = 4 * (w & 7);
+            const uint8_t* blk = raw + r * RB + 144 * bk;
+            const float d = h2f(ld16(blk)), dmin = h2f(ld16(blk + 2));
+            unsigned sc, mn;
+            scale_min_k4(2 * jj, blk + 4, sc, mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            scale_min_k4(2 * jj + 1, blk + 4, sc, mn);
+            const float d2 = d * (float)sc, m2 = dmin * (float)mn;
+            const unsigned q4 = *(const unsigned*)(blk + 16 + 4 * w);
+            const int e0 = 256 * bk + 64 * jj + l0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const unsigned byte = (q4 >> (8 * b)) & 0xFF;
+                put(r, e0 + b, (d1 * (float)(byte & 0xF) - m1) * xs[e0 + b]);
+                put(r, e0 + 32 + b, (d2 * (float)(byte >> 4) - m2) * xs[e0 + 32 + b]);
+            }
+        }
+    } else if constexpr (T == GG_Q6_K) {  // 8 rows x 2 blocks x 2 halves x 16 l-pairs: (d * sc) * q
+        for (int it = pt; it < 8 * 64; it += kProjProducers) {
+            const int r = it >> 6, bk = (it >> 5) & 1, h = (it >> 4) & 1, l = 2 * (it & 15);
+            const uint8_t* blk = raw + r * RB + 210 * bk;
+            const float d = h2f(ld16(blk + 208));
+            const unsigned la = ld16(blk + 64 * h + l), lb = ld16(blk + 64 * h + 32 + l);
+            const unsigned hb = ld16(blk + 128 + 32 * h + l);
+            const int e0 = 256 * bk + 128 * h + l;
+#pragma unroll
+            for (int quad = 0; quad < 4; quad++) {
+                const float ds = d * (float)(int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * quad];
+                const unsigned lq = (quad & 1) ? lb : la;
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    const unsigned lo = ((lq >> (8 * b)) >> (quad < 2 ? 0 : 4)) & 0xF;
+                    const unsigned hi = ((hb >> (8 * b)) >> (2 * quad)) & 3;
+                    const int q = (int)(lo | (hi << 4)) - 32;
+                    const int e = e0 + 32 * quad + b;
+                    put(r, e, ds * (float)q * xs[e]);
+                }
+            }
+        }
+    }
+}
+
+// s_waitcnt vmcnt(n) for a run-time n in [0, 15] (the count is an immediate)
+__device__ __forceinline__ void wait_loads_but(int n) {
+    switch (n) {
+#define PQA_VMCNT(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); break;
+        PQA_VMCNT(1) PQA_VMCNT(2) PQA_VMCNT(3) PQA_VMCNT(4) PQA_VMCNT(5) PQA_VMCNT(6) PQA_VMCNT(7)
+        PQA_VMCNT(8) PQA_VMCNT(9) PQA_VMCNT(10) PQA_VMCNT(11) PQA_VMCNT(12) PQA_VMCNT(13) PQA_VMCNT(14)
+        PQA_VMCNT(15)
+#undef PQA_VMCNT
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+static_assert(kProjDmaPerWave * (kProjSlots - 1) <= 15, "loads in flight exceed the waits written out");
+
+template <int T>
+__device__ void proj_wg(const ProjMat& m, const float* xs, uint8_t* ring, float* prod, int n, int lwg) {
+    constexpr int CE = QT<T>::CE, CB = QT<T>::CB;
+    constexpr int CDW = (CB + 3) / 4;  // dwords per row and chunk
+    constexpr int KC = CE / 8;         // chain elements per chunk
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int pt = tid - 64;  // producer thread index (waves 1-3)
+    const int row0 = lwg * kProjRows;
+    const int nch = (n + CE - 1) / CE;
+    const unsigned ring_lds = lds_addr(ring);
+    // Chunk t's rows go to slot t % kProjSlots as [row][CDW dwords]: 16 loads of
+    // 64 dwords, 4 per wave. Dword d: row d / CDW (rows past the matrix and the
+    // slot tail read clamped, unused data), word d % CDW (words past the row
+    // end stay inside its stride).
+    unsigned voff[kProjDmaPerWave];
+#pragma unroll
+    for (int i = 0; i < kProjDmaPerWave; i++) {
+        const int d = 64 * (kProjDmaPerWave * w + i) + lane;
+        const int rr = min(d / CDW, kProjRows - 1), wd = d - (d / CDW) * CDW;
+        voff[i] = (unsigned)(min(row0 + rr, m.rows - 1) * m.stride) + 4u * (unsigned)min(wd, CDW - 1);
+    }
+    auto issue = [&](int t) __attribute__((always_inline)) {
+        const unsigned slot = ring_lds + (unsigned)((t % kProjSlots) * kProjSlotBytes);
+#pragma unroll
+        for (int i = 0; i < kProjDmaPerWave; i++) {
+            // the last chunk of a row may end inside the row's 16-byte padding
+            const unsigned off = min(voff[i] + (unsigned)(t * CB),
+                                     voff[i] - voff[i] % (unsigned)m.stride + (unsigned)m.stride - 4u);
+            lds_dma_b32(m.w, off, slot + 256u * (unsigned)(kProjDmaPerWave * w + i));
+        }
+    };
+    // chain wave: lane (r, c)
+    const int r = lane >> 3, c = lane & 7;
+    float acc = 0.0f;
+    auto chains = [&](int t) __attribute__((always_inline)) {  // products of chunk t
+        const float* pr = prod + (t & 1) * 64 * kPS + (8 * r + c) * kPS;
+        const int ne = min(CE, n - t * CE);
+        if constexpr (T == GG_Q8_0) {  // lane c: block c; then d * sum into sumf in block order
+            const int nb = ne >> 5;
+            float sum = 0.0f;
+            if (c < nb) {
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) {
+                    const floatx4 p4 = *(const floatx4*)(pr + j);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) sum = sum + p4[b];
+                }
+            }
+            const float tb = pr[32] * sum;
+            for (int bi = 0; bi < nb; bi++) acc = acc + __shfl(tb, (lane & ~7) + bi);
+        } else if (ne == CE) {
+#pragma unroll
+            for (int k = 0; k < KC; k += 4) {
+                const floatx4 p4 = *(const floatx4*)(pr + k);
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc = acc + p4[b];
+            }
+        } else {
+            for (int k = 0; k < (ne >> 3); k++) acc = acc + pr[k];
+        }
+    };
+    for (int t = 0; t < kProjSlots - 1 && t < nch; t++) issue(t);
+    // step t: chunk t + 3 starts loading; producers turn chunk t into products
+    // while the chain wave sums chunk t - 1
+    for (int t = 0; t <= nch; t++) {
+        if (t < nch) {
+            if (t + kProjSlots - 1 < nch) issue(t + kProjSlots - 1);
+            // this wave's loads of chunk t are done once only those of later
+            // chunks (kProjDmaPerWave each) are outstanding
+            wait_loads_but(kProjDmaPerWave * min(kProjSlots - 1, nch - 1 - t));
+        }
+        __syncthreads();  // chunk t in its slot
+        if (w > 0) {
+            if (t < nch) produce<T>(ring + (t % kProjSlots) * kProjSlotBytes, xs + t * CE, prod + (t & 1) * 64 * kPS, pt);
+        } else if (t > 0) {
+            chains(t - 1);
+        }
+        __syncthreads();  // products of chunk t written, chunk t - 1 summed, slot t free
+    }
+    if (w == 0) {
+        float total;
+        if constexpr (T == GG_Q8_0) {
+            total = acc;
+        } else {
+            const float t4 = acc + __shfl(acc, lane + 4);  // lanes c < 4: acc0[c] + acc1[c]
+            const float t2 = t4 + __shfl(t4, lane + 2);    // c = 0: t0 + t2, c = 1: t1 + t3
+            total = t2 + __shfl(t2, lane + 1);             // c = 0: (t0 + t2) + (t1 + t3)
+        }
+        const int row = row0 + r;
+        if (c == 0 && row < m.rows) {
+            if (m.b) {
+                const float bv = m.btype == GG_F32 ? ((const float*)m.b)[row] : h2f(ld16(m.b + 2 * row));
+                total = total + bv;
+            }
+            m.out[row] = total;
+        }
+    }
+}
+
+// LDS: x [n] floats, the raw chunk ring (kProjSlots x 8 x kProjChunkMax
+// bytes) and two product buffers (64 x kPS floats each).
+__host__ __device__ inline size_t proj_x_bytes(int n) { return ((size_t)n * 4 + 15) / 16 * 16; }
+constexpr int kProjFixedLds = kProjSlots * kProjSlotBytes + 2 * 64 * kPS * 4;
+
+__global__ __launch_bounds__(64 * kProjWaves) void proj_kernel(const ProjArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* xs = (float*)smem;
+    for (int i = threadIdx.x; i < a.n; i += 64 * kProjWaves) xs[i] = a.x[i];
+    uint8_t* ring = smem + proj_x_bytes(a.n);
+    float* prod = (float*)(ring + kProjSlots * kProjSlotBytes);
+    int mi = 0;
+    while (mi + 1 < a.nmat && (int)blockIdx.x >= a.m[mi + 1].wg0) mi++;
+    const ProjMat& m = a.m[mi];
+    const int lwg = (int)blockIdx.x - m.wg0;
+    __syncthreads();
+    switch (m.wtype) {
+        case GG_F32: proj_wg<GG_F32>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_F16: proj_wg<GG_F16>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_Q4_0: proj_wg<GG_Q4_0>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_Q8_0: proj_wg<GG_Q8_0>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_Q4_K: proj_wg<GG_Q4_K>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_Q6_K: proj_wg<GG_Q6_K>(m, xs, ring, prod, a.n, lwg); break;
+        default: break;
+    }
+}
+
+size_t proj_lds_bytes(int n) { return proj_x_bytes(n) + kProjFixedLds; }
+
+}  // namespace pqa
+
+using pqa::hip_check;
+using pqa::set_err;
+
+namespace {
+
+int block_elems(int t) {
+    switch (t) {
+        case pqa::GG_F32: case pqa::GG_F16: return 1;
+        case pqa::GG_Q4_0: case pqa::GG_Q8_0: return 32;
+        case pqa::GG_Q4_K: case pqa::GG_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+int block_bytes(int t) {
+    switch (t) {
+        case pqa::GG_F32: return 4;
+        case pqa::GG_F16: return 2;
+        case pqa::GG_Q4_0: return 18;
+        case pqa::GG_Q8_0: return 34;
+        case pqa::GG_Q4_K: return 144;
+        case pqa::GG_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+// Rows are whole blocks; the chunk loop also needs whole 8-element groups
+// (F32/F16, no scalar tail) and 4-byte aligned chunk offsets (Q6_K rows of an
+// even number of blocks).
+const char* shape_problem(int t, int n) {
+    const int be = block_elems(t);
+    if (!be) return "unsupported weight type (F32, F16, Q4_0, Q8_0, Q4_K, Q6_K)";
+    if (n % be) return "n_embd is not a whole number of blocks";
+    if ((t == pqa::GG_F32 || t == pqa::GG_F16) && n % 8) return "F32/F16 rows need a multiple of 8 elements";
+    if (t == pqa::GG_Q6_K && n % 512) return "Q6_K rows need a multiple of 512 elements";
+    if ((t == pqa::GG_Q4_0 || t == pqa::GG_Q8_0) && n % 64) return "Q4_0/Q8_0 rows need a multiple of 64 elements";
+    return nullptr;
+}
+
+void free_proj(pqa_ctx* c, int layer) {
+    auto& p = c->proj[layer];
+    for (int i = 0; i < 3; i++) {
+        if (p.w[i]) (void)hipFree(p.w[i]);
+        if (p.b[i]) (void)hipFree(p.b[i]);
+        p.w[i] = p.b[i] = nullptr;
+    }
+    p.n_embd = 0;
+}
+
+}  // namespace
+
+void pqa_free_projections(pqa_ctx* c) {
+    for (int l = 0; l < (int)c->proj.size(); l++) free_proj(c, l);
+}
+
+extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wq, int wq_type, const void* bq,
+                                   int bq_type, const void* wk, int wk_type, const void* bk, int bk_type,
+                                   const void* wv, int wv_type, const void* bv, int bv_type) {
+    static const char* fn = "pqa_set_qkv_weights";
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_qkv_weights: ctx is NULL");
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, "pqa_set_qkv_weights: bad layer");
+    if (n_embd <= 0 || n_embd > PQA_MAX_EMBD)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED, "pqa_set_qkv_weights: n_embd outside [1, 8192]");
+    const void* w[3] = {wq, wk, wv};
+    const void* b[3] = {bq, bk, bv};
+    const int wt[3] = {wq_type, wk_type, wv_type};
+    const int bt[3] = {bq_type, bk_type, bv_type};
+    const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
+    for (int i = 0; i < 3; i++) {
+        if (!w[i]) return set_err(ctx, PQA_ERR_ARG, "pqa_set_qkv_weights: weight pointer is NULL");
+        if (const char* why = shape_problem(wt[i], n_embd))
+            return set_err(ctx, PQA_ERR_UNSUPPORTED, std::string(fn) + ": " + why);
+        if (b[i] && bt[i] != pqa::GG_NONE && bt[i] != pqa::GG_F32 && bt[i] != pqa::GG_F16)
+            return set_err(ctx, PQA_ERR_UNSUPPORTED, "pqa_set_qkv_weights: bias type must be F32 or F16");
+    }
+    if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
+    free_proj(ctx, layer);
+    auto& p = ctx->proj[layer];
+    for (int i = 0; i < 3; i++) {
+        const size_t rb = (size_t)(n_embd / block_elems(wt[i])) * block_bytes(wt[i]);
+        const size_t stride = (rb + 15) & ~(size_t)15;
+        // rows repacked at a 16-byte stride, plus a tail a chunk load may touch
+        if (int rc = hip_check(ctx, hipMalloc(&p.w[i], stride * rows[i] + 64), fn)) return free_proj(ctx, layer), rc;
+        if (int rc = hip_check(ctx, hipMemset(p.w[i], 0, stride * rows[i] + 64), fn)) return free_proj(ctx, layer), rc;
+        if (int rc = hip_check(ctx, hipMemcpy2D(p.w[i], stride, w[i], rb, rb, rows[i], hipMemcpyHostToDevice), fn))
+            return free_proj(ctx, layer), rc;
+        p.wtype[i] = wt[i];
+        p.stride[i] = (int)stride;
+        p.btype[i] = pqa::GG_NONE;
+        if (b[i] && bt[i] != pqa::GG_NONE) {
+            const size_t bb = (size_t)rows[i] * (bt[i] == pqa::GG_F32 ? 4 : 2);
+            if (int rc = hip_check(ctx, hipMalloc(&p.b[i], bb), fn)) return free_proj(ctx, layer), rc;
+            if (int rc = hip_check(ctx, hipMemcpy(p.b[i], b[i], bb, hipMemcpyHostToDevice), fn))
+                return free_proj(ctx, layer), rc;
+            p.btype[i] = bt[i];
+        }
+    }
+    p.n_embd = n_embd;
+    // x and the chunk rings can exceed the default 64 KB of dynamic LDS
+    const int lds = (int)pqa::proj_lds_bytes(n_embd);
+    return hip_check(ctx, hipFuncSetAttribute((const void*)pqa::proj_kernel,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds), fn);
+}
+
+namespace pqa {
+
+hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v) {
+    const auto& p = ctx->proj[layer];
+    ProjArgs a;
+    float* outs[3] = {q, k, v};
+    const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
+    int wgs = 0;
+    for (int i = 0; i < 3; i++) {
+        a.m[i].w = (const uint8_t*)p.w[i];
+        a.m[i].b = (const uint8_t*)p.b[i];
+        a.m[i].out = outs[i];
+        a.m[i].rows = rows[i];
+        a.m[i].wtype = p.wtype[i];
+        a.m[i].btype = p.btype[i];
+        a.m[i].stride = p.stride[i];
+        a.m[i].wg0 = wgs;
+        wgs += (rows[i] + kProjRows - 1) / kProjRows;
+    }
+    a.x = xb;
+    a.n = p.n_embd;
+    a.nmat = 3;
+    hipLaunchKernelGGL(proj_kernel, dim3(wgs), dim3(64 * kProjWaves), proj_lds_bytes(a.n), ctx->stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace pqa
+
+static int check_proj(pqa_ctx* ctx, int layer, const char* fn) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": bad layer");
+    if (ctx->proj.empty() || !ctx->proj[layer].n_embd)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": no projection weights for this layer");
+    return PQA_OK;
+}
+
+extern "C" int pqa_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v) {
+    if (int rc = check_proj(ctx, layer, "pqa_qkv_project")) return rc;
+    if (!xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project: NULL pointer");
+    return hip_check(ctx, pqa::launch_qkv_project(ctx, layer, xb, q, k, v), "pqa_qkv_project");
+}
+
+extern "C" int pqa_decode_x(pqa_ctx* ctx, int layer, int pos, const float* xb, float* out) {
+    if (int rc = check_proj(ctx, layer, "pqa_decode_x")) return rc;
+    if (!xb || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode_x: NULL pointer");
+    float* q = ctx->qkv;
+    float* k = q + ctx->q_dim;
+    float* v = k + ctx->kv_dim;
+    if (int rc = hip_check(ctx, pqa::launch_qkv_project(ctx, layer, xb, q, k, v), "pqa_decode_x")) return rc;
+    return pqa_decode(ctx, layer, pos, q, k, v, out);
+}

@@ -1,0 +1,133 @@
+"""Q/K/V projections on the GPU (pqa_qkv_project, pqa_decode_x through
+libpqa.so) against the projection oracle, which is bit-equal to the
+reference's matmul_bias: q, k and v bit-exact for every weight type, with and
+without biases, at small shapes and at the Qwen3-8B layer shape; the attention
+block from xb (pqa_decode_x) with its appended K/V rows bit-exact and its
+output within max-abs 2e-3 / rel 1e-2 of the oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import assert_bits_equal, assert_close
+from proj_cases import make_bias, make_rows
+
+torch = pytest.importorskip("torch")
+from picolm_qwen_amd import PicoAttention  # noqa: E402
+from picolm_qwen_amd._lib import PQA_ERR_ARG, PQA_ERR_UNSUPPORTED, PQAError  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TYPES = [O.GGUF_F32, O.GGUF_F16, O.GGUF_Q4_0, O.GGUF_Q8_0, O.GGUF_Q4_K, O.GGUF_Q6_K]
+
+
+def _project(att, layer, x):
+    dev = torch.device("cuda:0")
+    q, k, v = att.qkv_project(layer, torch.from_numpy(x).to(dev))
+    return q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+
+
+def _check(att, layer, x, mats):
+    got = _project(att, layer, x)
+    for name, g, (w, wt, rows, b, bt) in zip("qkv", got, mats):
+        want = O.matmul_bias(x, w, wt, rows, b, bt)
+        assert_bits_equal(g.view(np.uint32), want.view(np.uint32), f"{name} (type {wt}, bias {bt})")
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("n", [512, 1536])
+def test_projection_bit_exact_per_type(wtype, n):
+    print(f"projection type {wtype} n {n}", flush=True)
+    rng = np.random.default_rng(500 + 10 * wtype + n)
+    nh, nkv, hd = 8, 2, 64
+    att = PicoAttention(1, 64, nh, nkv, hd)
+    mats = []
+    for rows, bt in ((nh * hd, O.GGUF_NONE), (nkv * hd, O.GGUF_F32), (nkv * hd, O.GGUF_F16)):
+        b = None if bt == O.GGUF_NONE else make_bias(rng, bt, rows)
+        mats.append((make_rows(rng, wtype, rows, n, special=True), wtype, rows, b, bt))
+    (wq, _, _, bq, bqt), (wk, _, _, bk, bkt), (wv, _, _, bv, bvt) = mats
+    att.set_qkv_weights(0, n, wq, wtype, wk, wtype, wv, wtype, bq, bqt, bk, bkt, bv, bvt)
+    x = rng.standard_normal(n).astype(np.float32)
+    _check(att, 0, x, mats)
+    att.close()
+
+
+def test_projection_qwen3_8b_layer_mixed_types():
+    # Q4_K q/k and Q6_K v, as a Q4_K_M file stores them; 4096-wide rows
+    print("projection qwen3-8b layer", flush=True)
+    rng = np.random.default_rng(88)
+    nh, nkv, hd, n = 32, 8, 128, 4096
+    att = PicoAttention(2, 128, nh, nkv, hd)
+    mats = [(make_rows(rng, O.GGUF_Q4_K, nh * hd, n), O.GGUF_Q4_K, nh * hd, None, O.GGUF_NONE),
+            (make_rows(rng, O.GGUF_Q4_K, nkv * hd, n), O.GGUF_Q4_K, nkv * hd, None, O.GGUF_NONE),
+            (make_rows(rng, O.GGUF_Q6_K, nkv * hd, n), O.GGUF_Q6_K, nkv * hd, None, O.GGUF_NONE)]
+    att.set_qkv_weights(1, n, mats[0][0], O.GGUF_Q4_K, mats[1][0], O.GGUF_Q4_K, mats[2][0], O.GGUF_Q6_K)
+    for seed in range(2):
+        x = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+        _check(att, 1, x, mats)
+    att.close()
+
+
+@pytest.mark.parametrize("wtype", [O.GGUF_Q8_0, O.GGUF_Q4_0, O.GGUF_F16])
+def test_projection_qwen25_width_partial_chunk(wtype):
+    # Qwen2.5-0.5B: 896-wide rows (14 x 64), the last row chunk is partial
+    rng = np.random.default_rng(9 + wtype)
+    nh, nkv, hd, n = 14, 2, 64, 896
+    att = PicoAttention(1, 32, nh, nkv, hd)
+    mats = [(make_rows(rng, wtype, r, n), wtype, r, make_bias(rng, O.GGUF_F32, r), O.GGUF_F32)
+            for r in (nh * hd, nkv * hd, nkv * hd)]
+    att.set_qkv_weights(0, n, mats[0][0], wtype, mats[1][0], wtype, mats[2][0], wtype,
+                        mats[0][3], O.GGUF_F32, mats[1][3], O.GGUF_F32, mats[2][3], O.GGUF_F32)
+    x = rng.standard_normal(n).astype(np.float32)
+    _check(att, 0, x, mats)
+    att.close()
+
+
+def test_rejected_shapes_and_types():
+    att = PicoAttention(1, 16, 4, 2, 64)
+    w = np.zeros((256, 1024), np.uint8)
+    with pytest.raises(PQAError) as e:
+        att.set_qkv_weights(0, 1024, w, 10, w, 10, w, 10)  # Q8_1: not a type the reference dequantizes
+    assert e.value.code == PQA_ERR_UNSUPPORTED
+    with pytest.raises(PQAError) as e:
+        att.set_qkv_weights(0, 300, w, O.GGUF_Q4_K, w, O.GGUF_Q4_K, w, O.GGUF_Q4_K)  # not whole blocks
+    assert e.value.code == PQA_ERR_UNSUPPORTED
+    with pytest.raises(PQAError) as e:
+        att.set_qkv_weights(0, 256, w, O.GGUF_Q6_K, w, O.GGUF_Q6_K, w, O.GGUF_Q6_K)  # Q6_K needs 512
+    assert e.value.code == PQA_ERR_UNSUPPORTED
+    dev = torch.device("cuda:0")
+    with pytest.raises(PQAError) as e:
+        att.qkv_project(0, torch.zeros(256, device=dev))
+    assert e.value.code == PQA_ERR_ARG
+    att.close()
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_decode_from_xb_matches_oracle(qk_norm):
+    print(f"decode_x qk_norm {qk_norm}", flush=True)
+    rng = np.random.default_rng(77 + qk_norm)
+    nh, nkv, hd, n, smax, pos = 16, 8, 128, 2048, 512, 300
+    cos, sin = O.rope_table(1e6, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    qn = kn = None
+    if qk_norm:
+        qn, kn = O.qk_norm_weights(31, 0, hd)
+        att.set_qk_norm(0, qn, kn)
+    wq = make_rows(rng, O.GGUF_Q4_K, nh * hd, n)
+    wk = make_rows(rng, O.GGUF_Q4_K, nkv * hd, n)
+    wv = make_rows(rng, O.GGUF_Q6_K, nkv * hd, n)
+    att.set_qkv_weights(0, n, wq, O.GGUF_Q4_K, wk, O.GGUF_Q4_K, wv, O.GGUF_Q6_K)
+    att.synth_kv(0, 0, pos, 31, 0.0)
+    kc = np.zeros((smax, nkv * hd), np.uint16)
+    vc = np.zeros((smax, nkv * hd), np.uint16)
+    kc[:pos], vc[:pos] = O.synth_kv_rows(31, 0, nkv * hd, 0, pos)
+    x = rng.standard_normal(n).astype(np.float32)
+    q = O.matmul_bias(x, wq, O.GGUF_Q4_K, nh * hd)
+    k = O.matmul_bias(x, wk, O.GGUF_Q4_K, nkv * hd)
+    v = O.matmul_bias(x, wv, O.GGUF_Q6_K, nkv * hd)
+    shp = O.shape(nh, nkv, hd, smax, 0)
+    want = O.attn_step(shp, pos, q, k, v, qn, kn, cos[pos], sin[pos], kc, vc)
+    out = att.forward_x(0, pos, torch.from_numpy(x).to(torch.device("cuda:0"))).cpu().numpy()
+    gk, gv = att.kv_download(0, pos, 1)
+    assert_bits_equal(gk[0], kc[pos], "appended K row")
+    assert_bits_equal(gv[0], vc[pos], "appended V row")
+    assert_close(out, want)
+    att.close()
