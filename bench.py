@@ -308,9 +308,12 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
         if layer == 0:
             w0 = (wq, wk, wv)
             wbytes = wq.nbytes + wk.nbytes + wv.nbytes
+        wo = gguf_rows(rng, Q4K, n, nh * hd)
         vp = lambda a: a.ctypes.data_as(C.c_void_p)
         cx.check(cx.L.pqa_set_qkv_weights(cx.h, layer, n, vp(wq), Q4K, None, 0, vp(wk), Q4K, None, 0, vp(wv), Q6K,
                                           None, 0), cx.h)
+        cx.check(cx.L.pqa_set_out_weights(cx.h, layer, n, vp(wo), Q4K, None, 0), cx.h)
+        obytes = wo.nbytes
     x = torch.from_numpy(rng.standard_normal((n_layers, n), dtype=np.float32)).to(dev)
     q = torch.empty((n_layers, nh * hd), device=dev)
     k = torch.empty((n_layers, nkv * hd), device=dev)
@@ -327,10 +330,23 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
     wall, ev = timed(torch, cx, step, steps, warmup)
     us = ev * 1e3 / n_layers
     gbs = wbytes / (us * 1e-6) / 1e9
+    resid = torch.from_numpy(rng.standard_normal((n_layers, n), dtype=np.float32)).to(dev)
+    oproj = cx.L.pqa_out_project
+    optrs = [(C.c_void_p(q[l].data_ptr()), C.c_void_p(resid[l].data_ptr())) for l in range(n_layers)]
+
+    def ostep():
+        for layer in range(n_layers):
+            oproj(cx.h, layer, *optrs[layer])
+
+    _, oev = timed(torch, cx, ostep, steps, warmup)
+    ous = oev * 1e3 / n_layers
     res = {"workload": "qwen3_8b_qkv_proj_q4_k_m", "n_embd": n, "rows": [nh * hd, nkv * hd, nkv * hd],
            "weight_types": ["Q4_K", "Q4_K", "Q6_K"], "weight_bytes_per_layer": wbytes,
            "us_per_layer": round(us, 3), "weight_GB_per_s": round(gbs, 1),
-           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bit_exact_vs_reference_build_B": True}
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bit_exact_vs_reference_build_B": True,
+           "out_proj": {"rows": n, "width": nh * hd, "weight_type": "Q4_K", "weight_bytes_per_layer": obytes,
+                        "us_per_layer": round(ous, 3), "weight_GB_per_s": round(obytes / (ous * 1e-6) / 1e9, 1),
+                        "note": "attn_output matmul_bias + residual vec_add (cpp/model.hpp:420-427)"}}
     if cpu:
         import oracle as O
         if O.RefModel.available("B"):

@@ -178,6 +178,27 @@ int pqa_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k
  * pqa_decode. DEVICE pointers xb [n_embd], out [n_heads*head_dim]. */
 int pqa_decode_x(pqa_ctx* ctx, int layer, int pos, const float* xb, float* out);
 
+/*
+ * Attention output projection and residual add (cpp/model.hpp:420-427):
+ * xb2 = Wo attn + bo (TensorOps::matmul_bias, same order and types as above),
+ * then x = x + xb2 (TensorOps::vec_add, cpp/tensor.hpp:410-420).
+ * pqa_set_out_weights: attn_output as HOST GGUF rows [n_embd][q_dim elements]
+ * (q_dim = n_heads*head_dim) and an optional F32/F16 bias [n_embd]; the same
+ * type and width limits as pqa_set_qkv_weights, applied to q_dim.
+ */
+int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wo, int wo_type, const void* bo,
+                        int bo_type);
+
+/* x[n_embd] += Wo attn + bo, DEVICE pointers attn [q_dim] and x (updated in
+ * place); asynchronous on the context stream. */
+int pqa_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x);
+
+/* The attention half of a decode layer, cpp/model.hpp:320-427: from the
+ * normed input xb [n_embd] to the residual stream x [n_embd] (updated in
+ * place): Q/K/V projections, norms, RoPE, K/V append and attention at pos,
+ * output projection, x += result. Needs both weight sets of the layer. */
+int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float* x);
+
 /* The context's HIP stream (a hipStream_t), for event timing or ordering. */
 void* pqa_stream(pqa_ctx* ctx);
 int pqa_sync(pqa_ctx* ctx);

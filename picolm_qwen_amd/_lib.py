@@ -23,7 +23,8 @@ EXPORTS = [
     "pqa_prefill_host", "pqa_kv_upload", "pqa_kv_download", "pqa_kv_cache", "pqa_stream",
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
     "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
-    "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x",
+    "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x", "pqa_set_out_weights", "pqa_out_project",
+    "pqa_attention_block",
 ]
 
 
@@ -72,6 +73,9 @@ def lib() -> C.CDLL:
     L.pqa_set_qkv_weights.argtypes = [vp, i, i] + [vp, i, vp, i] * 3
     L.pqa_qkv_project.argtypes = [vp, i, vp, vp, vp, vp]
     L.pqa_decode_x.argtypes = [vp, i, i, vp, vp]
+    L.pqa_set_out_weights.argtypes = [vp, i, i, vp, i, vp, i]
+    L.pqa_out_project.argtypes = [vp, i, vp, vp]
+    L.pqa_attention_block.argtypes = [vp, i, i, vp, vp]
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int

@@ -260,6 +260,29 @@ class PicoAttention:
         self._leave(dev, ext)
         return out
 
+    def set_out_weights(self, layer: int, n_embd: int, wo, wo_type: int, bo=None, bo_type: int = 0) -> None:
+        """attn_output GGUF rows (uint8 [n_embd][row bytes of q_dim elements]) and an optional bias."""
+        wo = np.ascontiguousarray(wo)
+        b = None if bo is None else np.ascontiguousarray(bo)
+        check(lib().pqa_set_out_weights(self.handle, layer, n_embd, wo.ctypes.data_as(C.c_void_p), wo_type,
+                                        None if b is None else b.ctypes.data_as(C.c_void_p), bo_type), self.handle)
+
+    def out_project(self, layer: int, attn, x):
+        """x += Wo attn + bo (cpp/model.hpp:420-427); torch tensors on the device, x updated in place."""
+        ext = self._enter(attn.device, (attn, x))
+        check(lib().pqa_out_project(self.handle, layer, C.c_void_p(attn.data_ptr()), C.c_void_p(x.data_ptr())),
+              self.handle)
+        self._leave(attn.device, ext)
+        return x
+
+    def attention_block(self, layer: int, pos: int, xb, x):
+        """cpp/model.hpp:320-427 from the normed input xb: x += attn_output(attention(q, k, v))."""
+        ext = self._enter(xb.device, (xb, x))
+        check(lib().pqa_attention_block(self.handle, layer, pos, C.c_void_p(xb.data_ptr()), C.c_void_p(x.data_ptr())),
+              self.handle)
+        self._leave(xb.device, ext)
+        return x
+
     # -- .kvc persistence (picolm/model.c:870-983) ---------------------------
     def kvc_save(self, path: str, n_pos: int) -> None:
         """kvcache_save: rows [0, n_pos) of every layer to `path`; raises PQAError."""

@@ -108,7 +108,7 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     chk(dev_alloc(&c->qk_norm, (size_t)n_layers * 2 * head_dim), "qk norm");
     chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
     chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
-    chk(dev_alloc(&c->qkv, c->q_dim + 2 * c->kv_dim), "workspace");
+    chk(dev_alloc(&c->qkv, 2 * c->q_dim + 2 * c->kv_dim), "workspace");
     // one counter per decode column group; groups are single columns at most
     if (chk(dev_alloc(&c->tickets, (size_t)ny), "workspace")) chk(hipMemset(c->tickets, 0, (size_t)ny * 4), "memset");
     if (rc == PQA_OK) chk(hipDeviceSynchronize(), "sync");

@@ -15,13 +15,15 @@ namespace pqa {
 enum : int { GG_NONE = 0, GG_F32 = 1, GG_F16 = 2, GG_Q4_0 = 3, GG_Q8_0 = 9, GG_Q4_K = 13, GG_Q6_K = 15 };
 }
 
-// One layer's Q, K and V projection weights in HBM: GGUF rows at a 16-byte
-// stride, biases (F32 or F16) or null.
+// One layer's projection weights in HBM: GGUF rows at a 16-byte stride,
+// biases (F32 or F16) or null. Matrices 0-2: attn_q/k/v ([q_dim or kv_dim]
+// rows of n_embd); 3: attn_output ([n_embd] rows of q_dim).
 struct pqa_proj_weights {
-    void* w[3] = {nullptr, nullptr, nullptr};
-    void* b[3] = {nullptr, nullptr, nullptr};
-    int wtype[3] = {0, 0, 0}, btype[3] = {0, 0, 0}, stride[3] = {0, 0, 0};
-    int n_embd = 0;  // 0: not set
+    void* w[4] = {nullptr, nullptr, nullptr, nullptr};
+    void* b[4] = {nullptr, nullptr, nullptr, nullptr};
+    int wtype[4] = {0, 0, 0, 0}, btype[4] = {0, 0, 0, 0}, stride[4] = {0, 0, 0, 0};
+    int n_embd = 0;   // q/k/v set (row width); 0: not set
+    int out_rows = 0; // attn_output set (its row count, = n_embd); 0: not set
 };
 
 struct pqa_ctx {
@@ -51,7 +53,7 @@ struct pqa_ctx {
 
     // projections (pqa_set_qkv_weights) and the q/k/v of pqa_decode_x
     std::vector<pqa_proj_weights> proj;
-    float* qkv = nullptr;  // [q_dim + 2 kv_dim]
+    float* qkv = nullptr;  // [q_dim + 2 kv_dim + q_dim]: q, k, v and the attention output
 
     // staging for the _host entry points
     float* stage = nullptr;
@@ -83,6 +85,7 @@ hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const f
 hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
 hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
 hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);
+hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x);
 
 }  // namespace pqa
 

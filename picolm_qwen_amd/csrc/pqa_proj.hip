@@ -45,7 +45,8 @@ constexpr int kProjDmaPerWave = kProjSlotBytes / 256 / kProjWaves;
 struct ProjMat {
     const uint8_t* w;  // [rows][stride] GGUF rows
     const uint8_t* b;  // bias row or null
-    float* out;
+    float* out;        // with add_out: out[row] += result (vec_add into the residual stream)
+    int add_out;
     int rows, wtype, btype, stride, wg0;  // wg0: first workgroup of this matrix
 };
 
@@ -286,7 +287,7 @@ __device__ void proj_wg(const ProjMat& m, const float* xs, uint8_t* ring, float*
                 const float bv = m.btype == GG_F32 ? ((const float*)m.b)[row] : h2f(ld16(m.b + 2 * row));
                 total = total + bv;
             }
-            m.out[row] = total;
+            m.out[row] = m.add_out ? m.out[row] + total : total;
         }
     }
 }
@@ -363,18 +364,52 @@ const char* shape_problem(int t, int n) {
 
 void free_proj(pqa_ctx* c, int layer) {
     auto& p = c->proj[layer];
-    for (int i = 0; i < 3; i++) {
+    for (int i = 0; i < 4; i++) {
         if (p.w[i]) (void)hipFree(p.w[i]);
         if (p.b[i]) (void)hipFree(p.b[i]);
         p.w[i] = p.b[i] = nullptr;
     }
     p.n_embd = 0;
+    p.out_rows = 0;
 }
 
 }  // namespace
 
 void pqa_free_projections(pqa_ctx* c) {
     for (int l = 0; l < (int)c->proj.size(); l++) free_proj(c, l);
+}
+
+// Uploads matrix i of a layer: rows x GGUF rows of n elements, bias or null.
+static int upload_matrix(pqa_ctx* ctx, pqa_proj_weights& p, int i, const char* fn, int n, int rows, const void* w,
+                         int wt, const void* b, int bt) {
+    const size_t rb = (size_t)(n / block_elems(wt)) * block_bytes(wt);
+    const size_t stride = (rb + 15) & ~(size_t)15;
+    // rows repacked at a 16-byte stride, plus a tail a chunk load may touch
+    if (int rc = hip_check(ctx, hipMalloc(&p.w[i], stride * rows + 64), fn)) return rc;
+    if (int rc = hip_check(ctx, hipMemset(p.w[i], 0, stride * rows + 64), fn)) return rc;
+    if (int rc = hip_check(ctx, hipMemcpy2D(p.w[i], stride, w, rb, rb, rows, hipMemcpyHostToDevice), fn)) return rc;
+    p.wtype[i] = wt;
+    p.stride[i] = (int)stride;
+    p.btype[i] = pqa::GG_NONE;
+    if (b && bt != pqa::GG_NONE) {
+        const size_t bb = (size_t)rows * (bt == pqa::GG_F32 ? 4 : 2);
+        if (int rc = hip_check(ctx, hipMalloc(&p.b[i], bb), fn)) return rc;
+        if (int rc = hip_check(ctx, hipMemcpy(p.b[i], b, bb, hipMemcpyHostToDevice), fn)) return rc;
+        p.btype[i] = bt;
+    }
+    return PQA_OK;
+}
+
+static void free_matrix(pqa_proj_weights& p, int i) {
+    if (p.w[i]) (void)hipFree(p.w[i]);
+    if (p.b[i]) (void)hipFree(p.b[i]);
+    p.w[i] = p.b[i] = nullptr;
+}
+
+static int allow_lds(pqa_ctx* ctx, int n, const char* fn) {
+    // x and the chunk rings can exceed the default 64 KB of dynamic LDS
+    return hip_check(ctx, hipFuncSetAttribute((const void*)pqa::proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)pqa::proj_lds_bytes(n)), fn);
 }
 
 extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wq, int wq_type, const void* bq,
@@ -398,32 +433,41 @@ extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
             return set_err(ctx, PQA_ERR_UNSUPPORTED, "pqa_set_qkv_weights: bias type must be F32 or F16");
     }
     if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
-    free_proj(ctx, layer);
     auto& p = ctx->proj[layer];
-    for (int i = 0; i < 3; i++) {
-        const size_t rb = (size_t)(n_embd / block_elems(wt[i])) * block_bytes(wt[i]);
-        const size_t stride = (rb + 15) & ~(size_t)15;
-        // rows repacked at a 16-byte stride, plus a tail a chunk load may touch
-        if (int rc = hip_check(ctx, hipMalloc(&p.w[i], stride * rows[i] + 64), fn)) return free_proj(ctx, layer), rc;
-        if (int rc = hip_check(ctx, hipMemset(p.w[i], 0, stride * rows[i] + 64), fn)) return free_proj(ctx, layer), rc;
-        if (int rc = hip_check(ctx, hipMemcpy2D(p.w[i], stride, w[i], rb, rb, rows[i], hipMemcpyHostToDevice), fn))
-            return free_proj(ctx, layer), rc;
-        p.wtype[i] = wt[i];
-        p.stride[i] = (int)stride;
-        p.btype[i] = pqa::GG_NONE;
-        if (b[i] && bt[i] != pqa::GG_NONE) {
-            const size_t bb = (size_t)rows[i] * (bt[i] == pqa::GG_F32 ? 4 : 2);
-            if (int rc = hip_check(ctx, hipMalloc(&p.b[i], bb), fn)) return free_proj(ctx, layer), rc;
-            if (int rc = hip_check(ctx, hipMemcpy(p.b[i], b[i], bb, hipMemcpyHostToDevice), fn))
-                return free_proj(ctx, layer), rc;
-            p.btype[i] = bt[i];
+    for (int i = 0; i < 3; i++) free_matrix(p, i);
+    p.n_embd = 0;
+    for (int i = 0; i < 3; i++)
+        if (int rc = upload_matrix(ctx, p, i, fn, n_embd, rows[i], w[i], wt[i], b[i], bt[i])) {
+            for (int j = 0; j < 3; j++) free_matrix(p, j);
+            return rc;
         }
-    }
     p.n_embd = n_embd;
-    // x and the chunk rings can exceed the default 64 KB of dynamic LDS
-    const int lds = (int)pqa::proj_lds_bytes(n_embd);
-    return hip_check(ctx, hipFuncSetAttribute((const void*)pqa::proj_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds), fn);
+    return allow_lds(ctx, n_embd, fn);
+}
+
+extern "C" int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wo, int wo_type, const void* bo,
+                                   int bo_type) {
+    static const char* fn = "pqa_set_out_weights";
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_out_weights: ctx is NULL");
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, "pqa_set_out_weights: bad layer");
+    if (n_embd <= 0 || !wo) return set_err(ctx, PQA_ERR_ARG, "pqa_set_out_weights: bad n_embd or NULL weights");
+    const int width = (int)ctx->q_dim;  // attn_output rows are q_dim wide
+    if (width > PQA_MAX_EMBD)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED, "pqa_set_out_weights: n_heads * head_dim above 8192");
+    if (const char* why = shape_problem(wo_type, width))
+        return set_err(ctx, PQA_ERR_UNSUPPORTED, std::string(fn) + ": " + why);
+    if (bo && bo_type != pqa::GG_NONE && bo_type != pqa::GG_F32 && bo_type != pqa::GG_F16)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED, "pqa_set_out_weights: bias type must be F32 or F16");
+    if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
+    auto& p = ctx->proj[layer];
+    free_matrix(p, 3);
+    p.out_rows = 0;
+    if (int rc = upload_matrix(ctx, p, 3, fn, width, n_embd, wo, wo_type, bo, bo_type)) {
+        free_matrix(p, 3);
+        return rc;
+    }
+    p.out_rows = n_embd;
+    return allow_lds(ctx, width, fn);
 }
 
 namespace pqa {
@@ -438,6 +482,7 @@ hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q
         a.m[i].w = (const uint8_t*)p.w[i];
         a.m[i].b = (const uint8_t*)p.b[i];
         a.m[i].out = outs[i];
+        a.m[i].add_out = 0;
         a.m[i].rows = rows[i];
         a.m[i].wtype = p.wtype[i];
         a.m[i].btype = p.btype[i];
@@ -449,6 +494,26 @@ hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q
     a.n = p.n_embd;
     a.nmat = 3;
     hipLaunchKernelGGL(proj_kernel, dim3(wgs), dim3(64 * kProjWaves), proj_lds_bytes(a.n), ctx->stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x) {
+    const auto& p = ctx->proj[layer];
+    ProjArgs a;
+    a.m[0].w = (const uint8_t*)p.w[3];
+    a.m[0].b = (const uint8_t*)p.b[3];
+    a.m[0].out = x;
+    a.m[0].add_out = 1;
+    a.m[0].rows = p.out_rows;
+    a.m[0].wtype = p.wtype[3];
+    a.m[0].btype = p.btype[3];
+    a.m[0].stride = p.stride[3];
+    a.m[0].wg0 = 0;
+    a.x = attn;
+    a.n = (int)ctx->q_dim;
+    a.nmat = 1;
+    hipLaunchKernelGGL(proj_kernel, dim3((p.out_rows + kProjRows - 1) / kProjRows), dim3(64 * kProjWaves),
+                       proj_lds_bytes(a.n), ctx->stream, a);
     return hipGetLastError();
 }
 
@@ -476,4 +541,23 @@ extern "C" int pqa_decode_x(pqa_ctx* ctx, int layer, int pos, const float* xb, f
     float* v = k + ctx->kv_dim;
     if (int rc = hip_check(ctx, pqa::launch_qkv_project(ctx, layer, xb, q, k, v), "pqa_decode_x")) return rc;
     return pqa_decode(ctx, layer, pos, q, k, v, out);
+}
+
+extern "C" int pqa_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_out_project: ctx is NULL");
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, "pqa_out_project: bad layer");
+    if (ctx->proj.empty() || !ctx->proj[layer].out_rows)
+        return set_err(ctx, PQA_ERR_ARG, "pqa_out_project: no attn_output weights for this layer");
+    if (!attn || !x) return set_err(ctx, PQA_ERR_ARG, "pqa_out_project: NULL pointer");
+    return hip_check(ctx, pqa::launch_out_project(ctx, layer, attn, x), "pqa_out_project");
+}
+
+extern "C" int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float* x) {
+    if (int rc = check_proj(ctx, layer, "pqa_attention_block")) return rc;
+    if (!ctx->proj[layer].out_rows)
+        return set_err(ctx, PQA_ERR_ARG, "pqa_attention_block: no attn_output weights for this layer");
+    if (!xb || !x) return set_err(ctx, PQA_ERR_ARG, "pqa_attention_block: NULL pointer");
+    float* attn = ctx->qkv + ctx->q_dim + 2 * ctx->kv_dim;
+    if (int rc = pqa_decode_x(ctx, layer, pos, xb, attn)) return rc;
+    return hip_check(ctx, pqa::launch_out_project(ctx, layer, attn, x), "pqa_attention_block");
 }

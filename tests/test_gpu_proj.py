@@ -131,3 +131,61 @@ def test_decode_from_xb_matches_oracle(qk_norm):
     assert_bits_equal(gv[0], vc[pos], "appended V row")
     assert_close(out, want)
     att.close()
+
+
+@pytest.mark.parametrize("wtype,bt", [(O.GGUF_Q4_K, O.GGUF_NONE), (O.GGUF_Q8_0, O.GGUF_F32), (O.GGUF_F16, O.GGUF_F16),
+                                      (O.GGUF_Q6_K, O.GGUF_NONE)])
+def test_out_projection_with_residual_bit_exact(wtype, bt):
+    # Qwen3-4B shape: attention output 32 x 128 = 4096 wide, residual 2560
+    print(f"out projection type {wtype} bias {bt}", flush=True)
+    rng = np.random.default_rng(700 + wtype)
+    nh, nkv, hd, dim = 32, 8, 128, 2560
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    wo = make_rows(rng, wtype, dim, nh * hd)
+    bo = None if bt == O.GGUF_NONE else make_bias(rng, bt, dim)
+    att.set_out_weights(0, dim, wo, wtype, bo, bt)
+    dev = torch.device("cuda:0")
+    attn = rng.standard_normal(nh * hd).astype(np.float32)
+    x0 = rng.standard_normal(dim).astype(np.float32)
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.out_project(0, torch.from_numpy(attn).to(dev), x)
+    want = x0 + O.matmul_bias(attn, wo, wtype, dim, bo, bt)  # vec_add: x[i] + xb2[i] in fp32
+    assert_bits_equal(x.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32), "x after residual")
+    att.close()
+
+
+def test_attention_block_from_xb_to_residual():
+    # the whole attention half of a Qwen3-4B layer at pos 200: K/V rows
+    # bit-exact, x within the output tolerance (it carries the attention output)
+    print("attention block", flush=True)
+    rng = np.random.default_rng(4242)
+    nh, nkv, hd, dim, smax, pos = 32, 8, 128, 2560, 256, 200
+    cos, sin = O.rope_table(1e6, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    qn, kn = O.qk_norm_weights(5, 0, hd)
+    att.set_qk_norm(0, qn, kn)
+    wq = make_rows(rng, O.GGUF_Q4_K, nh * hd, dim)
+    wk = make_rows(rng, O.GGUF_Q4_K, nkv * hd, dim)
+    wv = make_rows(rng, O.GGUF_Q6_K, nkv * hd, dim)
+    wo = make_rows(rng, O.GGUF_Q4_K, dim, nh * hd)
+    att.set_qkv_weights(0, dim, wq, O.GGUF_Q4_K, wk, O.GGUF_Q4_K, wv, O.GGUF_Q6_K)
+    att.set_out_weights(0, dim, wo, O.GGUF_Q4_K)
+    att.synth_kv(0, 0, pos, 5, 0.0)
+    kc = np.zeros((smax, nkv * hd), np.uint16)
+    vc = np.zeros((smax, nkv * hd), np.uint16)
+    kc[:pos], vc[:pos] = O.synth_kv_rows(5, 0, nkv * hd, 0, pos)
+    xb = rng.standard_normal(dim).astype(np.float32)
+    x0 = rng.standard_normal(dim).astype(np.float32)
+    q = O.matmul_bias(xb, wq, O.GGUF_Q4_K, nh * hd)
+    k = O.matmul_bias(xb, wk, O.GGUF_Q4_K, nkv * hd)
+    v = O.matmul_bias(xb, wv, O.GGUF_Q6_K, nkv * hd)
+    attn = O.attn_step(O.shape(nh, nkv, hd, smax, 0), pos, q, k, v, qn, kn, cos[pos], sin[pos], kc, vc)
+    want = x0 + O.matmul_bias(attn, wo, O.GGUF_Q4_K, dim)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.attention_block(0, pos, torch.from_numpy(xb).to(dev), x)
+    gk, gv = att.kv_download(0, pos, 1)
+    assert_bits_equal(gk[0], kc[pos], "appended K row")
+    assert_bits_equal(gv[0], vc[pos], "appended V row")
+    assert_close(x.cpu().numpy(), want, what="residual stream")
+    att.close()
