@@ -16,6 +16,7 @@ Also reported in the same JSON line under "workloads":
   qwen2.5_0.5b_sweep  14/2/64, positions 0..4095 token by token, 24 layers
   qwen3_8b_kvc_save_load  .kvc save/load of 4096 positions x 36 layers (604 MB)
   qwen3_8b_qkv_proj   Q/K/V projections of one token, Q4_K/Q4_K/Q6_K, 36 layers
+  qwen3_4b_prefill_from_xb  prompt path from the normed inputs: projections + prefill
 
 `roofline` covers the decode kernel of the headline workload, timed with HIP
 events on the library's stream. `cpu_baseline` times the CPU oracle (the
@@ -371,6 +372,43 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
     return res
 
 
+def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, s=2048, steps=3, warmup=1):
+    """The prompt path of a Qwen3-4B-shaped layer from the normed inputs
+    (pqa_prefill_x): exact dequantization of Q4_K attn_q/attn_k and Q6_K
+    attn_v, three fp32 GEMMs over 2048 tokens (rocBLAS), bias, then the
+    K/V append and the causal MFMA prefill; 36 layers per step."""
+    Q4K, Q6K = 13, 15
+    cx = Ctx(n_layers, s, nh, nkv, hd, 0, 1e6)
+    rng = np.random.default_rng(909)
+    set_norms(cx, rng, hd)
+    vp = lambda a: a.ctypes.data_as(C.c_void_p)
+    for layer in range(n_layers):
+        wq, wk, wv = gguf_rows(rng, Q4K, nh * hd, dim), gguf_rows(rng, Q4K, nkv * hd, dim), gguf_rows(rng, Q6K, nkv * hd, dim)
+        cx.check(cx.L.pqa_set_qkv_weights(cx.h, layer, dim, vp(wq), Q4K, None, 0, vp(wk), Q4K, None, 0, vp(wv), Q6K,
+                                          None, 0), cx.h)
+    x = torch.from_numpy(rng.standard_normal((s, dim), dtype=np.float32)).to(dev)
+    out = torch.empty((s, nh * hd), device=dev)
+    torch.cuda.synchronize()
+    run = cx.L.pqa_prefill_x
+    xp, op = C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr())
+
+    def step():
+        for layer in range(n_layers):
+            cx.check(run(cx.h, layer, 0, s, xp, op), cx.h)
+
+    _, ev = timed(torch, cx, step, steps, warmup)
+    us = ev * 1e3 / n_layers
+    gemm_flops = 2.0 * s * (nh * hd + 2 * nkv * hd) * dim
+    attn_flops = prefill_flops(nh, hd, s)
+    cx.close()
+    res = {"workload": "qwen3_4b_prefill_from_xb", "tokens": s, "n_embd": dim, "weight_types": ["Q4_K", "Q4_K", "Q6_K"],
+           "us_per_layer": round(us, 1), "projection_GFLOP_per_layer": round(gemm_flops / 1e9, 1),
+           "attention_GFLOP_per_layer": round(attn_flops / 1e9, 1),
+           "TFLOP_per_s_total": round((gemm_flops + attn_flops) / (us * 1e-6) / 1e12, 1)}
+    log(f"[bench] prefill from xb: {us:.1f} us/layer; {res}")
+    return res
+
+
 def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
     """The oracle (reference attention loop, restated in C) on layer 0 of the
     headline cache: same K/V bytes (downloaded), same q/k/v and norm weights."""
@@ -523,7 +561,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
     ap.add_argument("--only", choices=["qwen3_1.7b_decode", "qwen3_4b_prefill", "tinyllama_decode",
-                                       "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load", "qwen3_8b_qkv_proj"],
+                                       "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load", "qwen3_8b_qkv_proj",
+                                       "qwen3_4b_prefill_from_xb"],
                     help="run one secondary workload and print it")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
@@ -557,6 +596,7 @@ def main():
             "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev),
             "qwen3_8b_kvc_save_load": lambda: kvc_workload(torch, dev),
             "qwen3_8b_qkv_proj": lambda: proj_workload(torch, dev, steps=args.steps, warmup=args.warmup),
+            "qwen3_4b_prefill_from_xb": lambda: prefill_x_workload(torch, dev),
         }
         print(json.dumps({args.only: runs[args.only]()}), flush=True)
         return
@@ -583,6 +623,7 @@ def main():
         workloads["qwen3_8b_kvc_save_load"] = kvc_workload(torch, dev)
         workloads["qwen3_8b_qkv_proj"] = proj_workload(torch, dev, steps=args.steps, warmup=args.warmup,
                                                        cpu=not args.no_cpu)
+        workloads["qwen3_4b_prefill_from_xb"] = prefill_x_workload(torch, dev)
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]

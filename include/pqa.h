@@ -199,6 +199,24 @@ int pqa_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x);
  * output projection, x += result. Needs both weight sets of the layer. */
 int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float* x);
 
+/*
+ * Q/K/V projections of a whole prompt (the per-token matmul_bias calls of
+ * Model::forward_batch, cpp/model.hpp:493-530) as one fp32 GEMM per matrix:
+ * the GGUF weights are dequantized exactly (dequantize_row_*), the GEMM runs
+ * in fp32 (rocBLAS), then the bias is added. Only the summation order differs
+ * from the reference, so q/k/v agree to fp32 rounding (about 1e-6 relative),
+ * not bit for bit (pqa_qkv_project keeps the order for one token). DEVICE
+ * pointers xb [n_tok][n_embd], q [n_tok][q_dim], k and v [n_tok][kv_dim];
+ * asynchronous on the context stream. The first call allocates a workspace of
+ * q_dim * n_embd floats and a rocBLAS handle.
+ */
+int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k, float* v);
+
+/* The prompt path of one layer from the normed inputs: pqa_qkv_project_batch
+ * into a context workspace (grown on demand), then pqa_prefill. DEVICE
+ * pointers xb [n_tok][n_embd], out [n_tok][n_heads*head_dim]. */
+int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* out);
+
 /* The context's HIP stream (a hipStream_t), for event timing or ordering. */
 void* pqa_stream(pqa_ctx* ctx);
 int pqa_sync(pqa_ctx* ctx);

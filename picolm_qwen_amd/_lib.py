@@ -24,7 +24,7 @@ EXPORTS = [
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
     "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
     "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x", "pqa_set_out_weights", "pqa_out_project",
-    "pqa_attention_block",
+    "pqa_attention_block", "pqa_qkv_project_batch", "pqa_prefill_x",
 ]
 
 
@@ -76,6 +76,8 @@ def lib() -> C.CDLL:
     L.pqa_set_out_weights.argtypes = [vp, i, i, vp, i, vp, i]
     L.pqa_out_project.argtypes = [vp, i, vp, vp]
     L.pqa_attention_block.argtypes = [vp, i, i, vp, vp]
+    L.pqa_qkv_project_batch.argtypes = [vp, i, i, vp, vp, vp, vp]
+    L.pqa_prefill_x.argtypes = [vp, i, i, i, vp, vp]
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int

@@ -283,6 +283,32 @@ class PicoAttention:
         self._leave(xb.device, ext)
         return x
 
+    def qkv_project_batch(self, layer: int, xb):
+        """q, k, v [n_tok][...] of a prompt (fp32 GEMMs over exactly dequantized weights)."""
+        import torch
+        n_tok = xb.shape[0]
+        dev = xb.device
+        q = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=dev)
+        k = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
+        v = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
+        ext = self._enter(dev, (xb, q, k, v))
+        check(lib().pqa_qkv_project_batch(self.handle, layer, n_tok, C.c_void_p(xb.data_ptr()),
+                                          C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
+                                          C.c_void_p(v.data_ptr())), self.handle)
+        self._leave(dev, ext)
+        return q, k, v
+
+    def forward_batch_x(self, layer: int, start_pos: int, xb, out=None):
+        """The prompt path of a layer from the normed inputs xb [n_tok][n_embd]."""
+        import torch
+        n_tok = xb.shape[0]
+        out = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=xb.device) if out is None else out
+        ext = self._enter(xb.device, (xb, out))
+        check(lib().pqa_prefill_x(self.handle, layer, start_pos, n_tok, C.c_void_p(xb.data_ptr()),
+                                  C.c_void_p(out.data_ptr())), self.handle)
+        self._leave(xb.device, ext)
+        return out
+
     # -- .kvc persistence (picolm/model.c:870-983) ---------------------------
     def kvc_save(self, path: str, n_pos: int) -> None:
         """kvcache_save: rows [0, n_pos) of every layer to `path`; raises PQAError."""

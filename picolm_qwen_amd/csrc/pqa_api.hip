@@ -33,8 +33,9 @@ static void free_ctx(pqa_ctx* c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     pqa_free_projections(c);
-    void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm,
-                    c->part_acc,  c->part_ml,   c->stage,   c->tickets,  c->qkv};
+    pqa_free_batch(c);
+    void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm, c->part_acc,
+                    c->part_ml,   c->stage,     c->tickets,  c->qkv,      c->bqkv};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int i = 0; i < 2; ++i) {

@@ -55,6 +55,14 @@ struct pqa_ctx {
     std::vector<pqa_proj_weights> proj;
     float* qkv = nullptr;  // [q_dim + 2 kv_dim + q_dim]: q, k, v and the attention output
 
+    // batched projections (pqa_batch.hip): rocBLAS handle, fp32 weights of one
+    // matrix, q/k/v of pqa_prefill_x; made on first use
+    void* blas = nullptr;
+    float* wf32 = nullptr;
+    size_t wf32_floats = 0;
+    float* bqkv = nullptr;
+    size_t bqkv_floats = 0;
+
     // staging for the _host entry points
     float* stage = nullptr;
     size_t stage_floats = 0;
@@ -91,3 +99,6 @@ hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float*
 
 // Frees every layer's projection weights (pqa_proj.hip).
 void pqa_free_projections(pqa_ctx* c);
+
+// Releases the rocBLAS handle and the fp32 weight workspace (pqa_batch.hip).
+void pqa_free_batch(pqa_ctx* c);

@@ -8,6 +8,11 @@ import oracle as O
 
 # byte offsets of the fp16 scale fields inside one block (cpp/quant.hpp:33-63)
 SCALE_FIELDS = {O.GGUF_Q4_0: (0,), O.GGUF_Q8_0: (0,), O.GGUF_Q4_K: (0, 2), O.GGUF_Q6_K: (208,)}
+# scale ranges that keep |w| at most about 0.2, as in trained models (the
+# integer sub-scales and quants multiply them: Q4_0 8, Q8_0 128, Q4_K 63 * 15,
+# Q6_K 127 * 32)
+SCALE_RANGE = {O.GGUF_Q4_0: (1e-3, 2e-2), O.GGUF_Q8_0: (1e-4, 1.5e-3), O.GGUF_Q4_K: (1e-5, 2e-4),
+               O.GGUF_Q6_K: (1e-6, 5e-5)}
 SPECIAL_F16 = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x8123, 0xBC00], np.uint16)  # 0, -0, subnormals, -1
 
 
@@ -21,7 +26,8 @@ def make_rows(rng, wtype, rows, n, special=False):
         return (rng.standard_normal((rows, n)) * 0.05).astype("<f2").view(np.uint8).reshape(rows, -1)
     raw = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
     for off in SCALE_FIELDS[wtype]:
-        scale = (rng.uniform(1e-3, 2e-2, (rows, nb)) * rng.choice([1.0, -1.0], (rows, nb))).astype("<f2")
+        lo, hi = SCALE_RANGE[wtype]
+        scale = (rng.uniform(lo, hi, (rows, nb)) * rng.choice([1.0, -1.0], (rows, nb))).astype("<f2")
         raw[:, :, off:off + 2] = scale.view(np.uint8).reshape(rows, nb, 2)
         if special:
             sel = rng.random((rows, nb)) < 0.2

@@ -189,3 +189,66 @@ def test_attention_block_from_xb_to_residual():
     assert_bits_equal(gv[0], vc[pos], "appended V row")
     assert_close(x.cpu().numpy(), want, what="residual stream")
     att.close()
+
+
+def test_batched_projection_within_fp32_reordering_bound():
+    # Qwen3-4B widths, 37 tokens: the weights are dequantized exactly, only
+    # the order of each dot product's sum differs, so |got - ref| <=
+    # 2 (n + 1) 2^-24 sum_i |w_i x_i| (product rounding and any summation
+    # order, both sides)
+    print("batched projection", flush=True)
+    rng = np.random.default_rng(31337)
+    nh, nkv, hd, dim, n_tok = 32, 8, 128, 2560, 37
+    att = PicoAttention(1, 64, nh, nkv, hd)
+    mats = [(make_rows(rng, O.GGUF_Q4_K, nh * hd, dim), O.GGUF_Q4_K, nh * hd, make_bias(rng, O.GGUF_F32, nh * hd),
+             O.GGUF_F32),
+            (make_rows(rng, O.GGUF_Q4_K, nkv * hd, dim), O.GGUF_Q4_K, nkv * hd, None, O.GGUF_NONE),
+            (make_rows(rng, O.GGUF_Q6_K, nkv * hd, dim), O.GGUF_Q6_K, nkv * hd, make_bias(rng, O.GGUF_F16, nkv * hd),
+             O.GGUF_F16)]
+    att.set_qkv_weights(0, dim, mats[0][0], O.GGUF_Q4_K, mats[1][0], O.GGUF_Q4_K, mats[2][0], O.GGUF_Q6_K,
+                        mats[0][3], O.GGUF_F32, None, 0, mats[2][3], O.GGUF_F16)
+    x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    got = [g.cpu().numpy() for g in att.qkv_project_batch(0, torch.from_numpy(x).to(torch.device("cuda:0")))]
+    for name, g, (w, wt, rows, b, bt) in zip("qkv", got, mats):
+        wf = np.stack([O.dequant_row(wt, w[r], dim) for r in range(rows)]).astype(np.float64)
+        for t in range(0, n_tok, 6):
+            want = O.matmul_bias(x[t], w, wt, rows, b, bt)
+            bound = 2.0 * (dim + 1) * 2.0 ** -24 * (np.abs(wf) @ np.abs(x[t].astype(np.float64))) + 1e-30
+            err = np.abs(g[t].astype(np.float64) - want)
+            assert np.all(err <= bound), (name, t, float(np.max(err / bound)))
+    att.close()
+
+
+def test_prompt_path_from_xb_matches_oracle():
+    # pqa_prefill_x = batched projections + the MFMA prefill: outputs within the
+    # attention tolerance; K rows carry the projection's reordering, so a few
+    # elements may round to the neighbouring fp16 value
+    print("prefill_x", flush=True)
+    rng = np.random.default_rng(2718)
+    nh, nkv, hd, dim, n_tok, smax = 16, 8, 128, 2048, 96, 128
+    cos, sin = O.rope_table(1e6, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    qn, kn = O.qk_norm_weights(9, 0, hd)
+    att.set_qk_norm(0, qn, kn)
+    wq = make_rows(rng, O.GGUF_Q4_K, nh * hd, dim)
+    wk = make_rows(rng, O.GGUF_Q4_K, nkv * hd, dim)
+    wv = make_rows(rng, O.GGUF_Q6_K, nkv * hd, dim)
+    att.set_qkv_weights(0, dim, wq, O.GGUF_Q4_K, wk, O.GGUF_Q4_K, wv, O.GGUF_Q6_K)
+    x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    q = np.stack([O.matmul_bias(x[t], wq, O.GGUF_Q4_K, nh * hd) for t in range(n_tok)])
+    k = np.stack([O.matmul_bias(x[t], wk, O.GGUF_Q4_K, nkv * hd) for t in range(n_tok)])
+    v = np.stack([O.matmul_bias(x[t], wv, O.GGUF_Q6_K, nkv * hd) for t in range(n_tok)])
+    kc = np.zeros((smax, nkv * hd), np.uint16)
+    vc = np.zeros((smax, nkv * hd), np.uint16)
+    want = O.prefill(O.shape(nh, nkv, hd, smax, 0), 0, q, k, v, qn, kn, cos, sin, kc, vc)
+    out = att.forward_batch_x(0, 0, torch.from_numpy(x).to(torch.device("cuda:0"))).cpu().numpy()
+    assert_close(out, want)
+    gk, gv = att.kv_download(0, 0, n_tok)
+    for name, g, wnt in (("K", gk, kc[:n_tok]), ("V", gv, vc[:n_tok])):
+        same = g == wnt
+        gf, wf = g.view(np.float16).astype(np.float64), wnt.view(np.float16).astype(np.float64)
+        # one fp16 rounding of the value, plus the projection's reordering
+        # (1e-6 relative to the row scale) carried through norm and RoPE
+        slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
+        assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
+    att.close()
