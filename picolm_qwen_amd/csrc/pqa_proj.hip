@@ -20,9 +20,12 @@
 // HBM into a 4-slot LDS ring by direct global->LDS loads (chunk t + 3 in
 // flight while t is used); waves 1-15 turn chunk t into fp32 products
 // round(w * x) in LDS, chain-major (Q8_0: block-major with each block's d),
-// while wave 0, lane 8 r + c, adds chunk t - 1 into chain c of row r. Two
-// barriers per chunk. The work is VALU- and latency-bound by the fixed order
-// (no MFMA or packed math can keep it).
+// while wave 0, lane 8 r + c, adds chunk t - 1 into chain c of row r. One
+// barrier per chunk. Each producer item issues all its LDS reads (quant
+// bytes, scales, x) before its first product store, since the compiler
+// cannot move a read of x past a store into the same LDS block. The work is
+// VALU- and latency-bound by the fixed order (no MFMA or packed math can
+// keep it).
 #include <algorithm>
 #include <cstring>
 #include <string>
@@ -69,14 +72,20 @@ template <> struct QT<GG_Q8_0> { static constexpr int CE = 256, CB = 272; };
 template <> struct QT<GG_Q4_K> { static constexpr int CE = 512, CB = 288; };
 template <> struct QT<GG_Q6_K> { static constexpr int CE = 512, CB = 420; };
 
-// get_scale_min_k4 (cpp/quant.hpp:210-218)
-__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, unsigned& sc, unsigned& mn) {
+// get_scale_min_k4 (cpp/quant.hpp:210-218) on the 12 scale bytes held as
+// three little-endian words
+__device__ __forceinline__ unsigned scale_byte(unsigned s0, unsigned s1, unsigned s2, int i) {
+    const unsigned wd = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (wd >> (8 * (i & 3))) & 0xFF;
+}
+__device__ __forceinline__ void scale_min_k4_regs(int j, unsigned s0, unsigned s1, unsigned s2, unsigned& sc,
+                                                  unsigned& mn) {
     if (j < 4) {
-        sc = q[j] & 63;
-        mn = q[j + 4] & 63;
+        sc = scale_byte(s0, s1, s2, j) & 63;
+        mn = scale_byte(s0, s1, s2, j + 4) & 63;
     } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        sc = (scale_byte(s0, s1, s2, j + 4) & 0xF) | ((scale_byte(s0, s1, s2, j - 4) >> 6) << 4);
+        mn = (scale_byte(s0, s1, s2, j + 4) >> 4) | ((scale_byte(s0, s1, s2, j) >> 6) << 4);
     }
 }
 
@@ -112,66 +121,86 @@ __device__ __forceinline__ void produce(const uint8_t* raw, const float* xs, flo
         for (int it = pt; it < 8 * 128; it += kProjProducers) {
             const int r = it >> 7, bi = (it >> 3) & 15, j2 = 2 * (it & 7);
             const uint8_t* blk = raw + r * RB + 18 * bi;
-            const float d = h2f(ld16(blk));
-            const unsigned two = ld16(blk + 2 + j2);
+            const int e = 32 * bi + j2;
+            const unsigned dh = ld16(blk), two = ld16(blk + 2 + j2);
+            const float2 xl = *(const float2*)(xs + e), xh = *(const float2*)(xs + e + 16);
+            const float d = h2f(dh);
+            const float xlo[2] = {xl.x, xl.y}, xhi[2] = {xh.x, xh.y};
 #pragma unroll
             for (int b = 0; b < 2; b++) {
                 const unsigned byte = (two >> (8 * b)) & 0xFF;
-                const int e = 32 * bi + j2 + b;
-                put(r, e, d * ((float)(byte & 0xF) - 8.0f) * xs[e]);
-                put(r, e + 16, d * ((float)(byte >> 4) - 8.0f) * xs[e + 16]);
+                put(r, e + b, d * ((float)(byte & 0xF) - 8.0f) * xlo[b]);
+                put(r, e + b + 16, d * ((float)(byte >> 4) - 8.0f) * xhi[b]);
             }
         }
     } else if constexpr (T == GG_Q8_0) {  // 8 rows x 8 blocks x 8 groups of 4: (float)q * x
         for (int it = pt; it < 8 * 64; it += kProjProducers) {
             const int r = it >> 6, bi = (it >> 3) & 7, g = it & 7;
             const uint8_t* blk = raw + r * RB + 34 * bi;
-            const unsigned lo = ld16(blk + 2 + 4 * g), hi = ld16(blk + 4 + 4 * g);
+            const unsigned lo = ld16(blk + 2 + 4 * g), hi = ld16(blk + 4 + 4 * g), dh = ld16(blk);
+            const floatx4 x = *(const floatx4*)(xs + 32 * bi + 4 * g);
             const unsigned q4 = lo | (hi << 16);
             float* pr = prod + (8 * r + bi) * kPS;
+            floatx4 v;
 #pragma unroll
-            for (int b = 0; b < 4; b++)
-                pr[4 * g + b] = (float)(int)(int8_t)((q4 >> (8 * b)) & 0xFF) * xs[32 * bi + 4 * g + b];
-            if (g == 0) pr[32] = h2f(ld16(blk));
+            for (int b = 0; b < 4; b++) v[b] = (float)(int)(int8_t)((q4 >> (8 * b)) & 0xFF) * x[b];
+            *(floatx4*)(pr + 4 * g) = v;
+            if (g == 0) pr[32] = h2f(dh);
         }
     } else if constexpr (T == GG_Q4_K) {  // 8 rows x 2 blocks x 32 qs dwords: (d * sc) * q - dmin * mn
         for (int it = pt; it < 8 * 64; it += kProjProducers) {
             const int r = it >> 6, bk = (it >> 5) & 1, w = it & 31, jj = w >> 3, l0 = 4 * (w & 7);
             const uint8_t* blk = raw + r * RB + 144 * bk;
-            const float d = h2f(ld16(blk)), dmin = h2f(ld16(blk + 2));
-            unsigned sc, mn;
-            scale_min_k4(2 * jj, blk + 4, sc, mn);
-            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
-            scale_min_k4(2 * jj + 1, blk + 4, sc, mn);
-            const float d2 = d * (float)sc, m2 = dmin * (float)mn;
-            const unsigned q4 = *(const unsigned*)(blk + 16 + 4 * w);
             const int e0 = 256 * bk + 64 * jj + l0;
+            // every LDS read of the item first (d and dmin, the 12 scale bytes,
+            // the 4 quant bytes, x), so they share one round trip
+            const unsigned dd = *(const unsigned*)blk;
+            const unsigned s0 = *(const unsigned*)(blk + 4), s1 = *(const unsigned*)(blk + 8),
+                           s2 = *(const unsigned*)(blk + 12);
+            const unsigned q4 = *(const unsigned*)(blk + 16 + 4 * w);
+            const floatx4 xa = *(const floatx4*)(xs + e0), xb = *(const floatx4*)(xs + e0 + 32);
+            const float d = h2f(dd & 0xFFFF), dmin = h2f(dd >> 16);
+            unsigned sc, mn;
+            scale_min_k4_regs(2 * jj, s0, s1, s2, sc, mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            scale_min_k4_regs(2 * jj + 1, s0, s1, s2, sc, mn);
+            const float d2 = d * (float)sc, m2 = dmin * (float)mn;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const unsigned byte = (q4 >> (8 * b)) & 0xFF;
-                put(r, e0 + b, (d1 * (float)(byte & 0xF) - m1) * xs[e0 + b]);
-                put(r, e0 + 32 + b, (d2 * (float)(byte >> 4) - m2) * xs[e0 + 32 + b]);
+                put(r, e0 + b, (d1 * (float)(byte & 0xF) - m1) * xa[b]);
+                put(r, e0 + 32 + b, (d2 * (float)(byte >> 4) - m2) * xb[b]);
             }
         }
     } else if constexpr (T == GG_Q6_K) {  // 8 rows x 2 blocks x 2 halves x 16 l-pairs: (d * sc) * q
         for (int it = pt; it < 8 * 64; it += kProjProducers) {
             const int r = it >> 6, bk = (it >> 5) & 1, h = (it >> 4) & 1, l = 2 * (it & 15);
             const uint8_t* blk = raw + r * RB + 210 * bk;
-            const float d = h2f(ld16(blk + 208));
+            const int e0 = 256 * bk + 128 * h + l;
+            // every LDS read of the item first: d, the quant bytes, the four
+            // scale pairs (scale of quad q is byte l / 16 of pair q) and x
+            const unsigned dh = ld16(blk + 208);
             const unsigned la = ld16(blk + 64 * h + l), lb = ld16(blk + 64 * h + 32 + l);
             const unsigned hb = ld16(blk + 128 + 32 * h + l);
-            const int e0 = 256 * bk + 128 * h + l;
+            unsigned sp[4];
+            float2 xv[4];
 #pragma unroll
             for (int quad = 0; quad < 4; quad++) {
-                const float ds = d * (float)(int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * quad];
+                sp[quad] = ld16(blk + 192 + 8 * h + 2 * quad);
+                xv[quad] = *(const float2*)(xs + e0 + 32 * quad);
+            }
+            const float d = h2f(dh);
+#pragma unroll
+            for (int quad = 0; quad < 4; quad++) {
+                const float ds = d * (float)(int)(int8_t)((sp[quad] >> (8 * (l >> 4))) & 0xFF);
                 const unsigned lq = (quad & 1) ? lb : la;
+                const float xq[2] = {xv[quad].x, xv[quad].y};
 #pragma unroll
                 for (int b = 0; b < 2; b++) {
                     const unsigned lo = ((lq >> (8 * b)) >> (quad < 2 ? 0 : 4)) & 0xF;
                     const unsigned hi = ((hb >> (8 * b)) >> (2 * quad)) & 3;
                     const int q = (int)(lo | (hi << 4)) - 32;
-                    const int e = e0 + 32 * quad + b;
-                    put(r, e, ds * (float)q * xs[e]);
+                    put(r, e0 + 32 * quad + b, ds * (float)q * xq[b]);
                 }
             }
         }
@@ -192,7 +221,8 @@ __device__ __forceinline__ void wait_loads_but(int n) {
 static_assert(kProjDmaPerWave * (kProjSlots - 1) <= 15, "loads in flight exceed the waits written out");
 
 template <int T>
-__device__ void proj_wg(const ProjMat& m, const float* xs, uint8_t* ring, float* prod, int n, int lwg) {
+__device__ void proj_wg(const ProjMat& m, const float* __restrict__ x, float* xs, uint8_t* ring, float* prod, int n,
+                        int lwg) {
     constexpr int CE = QT<T>::CE, CB = QT<T>::CB;
     constexpr int CDW = (CB + 3) / 4;  // dwords per row and chunk
     constexpr int KC = CE / 8;         // chain elements per chunk
@@ -255,22 +285,27 @@ __device__ void proj_wg(const ProjMat& m, const float* xs, uint8_t* ring, float*
         }
     };
     for (int t = 0; t < kProjSlots - 1 && t < nch; t++) issue(t);
-    // step t: chunk t + 3 starts loading; producers turn chunk t into products
-    // while the chain wave sums chunk t - 1
+    // x goes to LDS while the first chunks load (loads complete in issue
+    // order, so its wait covers them too: one round trip for both)
+    for (int i = tid; i < n; i += 64 * kProjWaves) xs[i] = x[i];
+    // this wave's loads of chunk t are done once only those of later chunks
+    // (kProjDmaPerWave each) are outstanding
+    wait_loads_but(kProjDmaPerWave * min(kProjSlots - 2, nch - 1));
+    __syncthreads();  // x and chunk 0 in LDS
+    // step t: chunk t + 3 starts loading into the slot chunk t - 1 left;
+    // producers turn chunk t into products while the chain wave sums chunk
+    // t - 1; every wave then waits for its loads of chunk t + 1, and one
+    // barrier publishes the products, ends the reads of chunk t - 1's products
+    // and makes chunk t + 1 visible
     for (int t = 0; t <= nch; t++) {
-        if (t < nch) {
-            if (t + kProjSlots - 1 < nch) issue(t + kProjSlots - 1);
-            // this wave's loads of chunk t are done once only those of later
-            // chunks (kProjDmaPerWave each) are outstanding
-            wait_loads_but(kProjDmaPerWave * min(kProjSlots - 1, nch - 1 - t));
-        }
-        __syncthreads();  // chunk t in its slot
+        if (t + kProjSlots - 1 < nch) issue(t + kProjSlots - 1);
         if (w > 0) {
             if (t < nch) produce<T>(ring + (t % kProjSlots) * kProjSlotBytes, xs + t * CE, prod + (t & 1) * 64 * kPS, pt);
         } else if (t > 0) {
             chains(t - 1);
         }
-        __syncthreads();  // products of chunk t written, chunk t - 1 summed, slot t free
+        if (t + 1 < nch) wait_loads_but(kProjDmaPerWave * min(kProjSlots - 2, nch - 2 - t));
+        __syncthreads();
     }
     if (w == 0) {
         float total;
@@ -300,21 +335,19 @@ constexpr int kProjFixedLds = kProjSlots * kProjSlotBytes + 2 * 64 * kPS * 4;
 __global__ __launch_bounds__(64 * kProjWaves) void proj_kernel(const ProjArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float* xs = (float*)smem;
-    for (int i = threadIdx.x; i < a.n; i += 64 * kProjWaves) xs[i] = a.x[i];
     uint8_t* ring = smem + proj_x_bytes(a.n);
     float* prod = (float*)(ring + kProjSlots * kProjSlotBytes);
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.m[mi + 1].wg0) mi++;
     const ProjMat& m = a.m[mi];
     const int lwg = (int)blockIdx.x - m.wg0;
-    __syncthreads();
     switch (m.wtype) {
-        case GG_F32: proj_wg<GG_F32>(m, xs, ring, prod, a.n, lwg); break;
-        case GG_F16: proj_wg<GG_F16>(m, xs, ring, prod, a.n, lwg); break;
-        case GG_Q4_0: proj_wg<GG_Q4_0>(m, xs, ring, prod, a.n, lwg); break;
-        case GG_Q8_0: proj_wg<GG_Q8_0>(m, xs, ring, prod, a.n, lwg); break;
-        case GG_Q4_K: proj_wg<GG_Q4_K>(m, xs, ring, prod, a.n, lwg); break;
-        case GG_Q6_K: proj_wg<GG_Q6_K>(m, xs, ring, prod, a.n, lwg); break;
+        case GG_F32: proj_wg<GG_F32>(m, a.x, xs, ring, prod, a.n, lwg); break;
+        case GG_F16: proj_wg<GG_F16>(m, a.x, xs, ring, prod, a.n, lwg); break;
+        case GG_Q4_0: proj_wg<GG_Q4_0>(m, a.x, xs, ring, prod, a.n, lwg); break;
+        case GG_Q8_0: proj_wg<GG_Q8_0>(m, a.x, xs, ring, prod, a.n, lwg); break;
+        case GG_Q4_K: proj_wg<GG_Q4_K>(m, a.x, xs, ring, prod, a.n, lwg); break;
+        case GG_Q6_K: proj_wg<GG_Q6_K>(m, a.x, xs, ring, prod, a.n, lwg); break;
         default: break;
     }
 }
