@@ -528,14 +528,17 @@ def summarize_trace(trace_dir):
     groups = {}
     for r in _rows(_find(trace_dir, "kernel_trace.csv")):
         name = r["Kernel_Name"]
-        if not name.startswith("void pqa::"):
+        # this library's kernels, and rocBLAS's GEMM kernels of the batched projections
+        if not name.startswith(("void pqa::", "pqa::", "Cijk_")):
             continue
         grid = tuple(int(r.get(f"Grid_Size_{a}", r.get("Grid_Size", 0)) or 0) for a in "XYZ")
         g = groups.setdefault((name, grid), [])
         g.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     lines = [f"{'kernel':52s} {'grid (threads)':>20s} {'calls':>7s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        short = name.replace("void pqa::", "").split("(")[0]
+        short = name.replace("void pqa::", "").replace("pqa::", "").split("(")[0]
+        if short.startswith("Cijk_"):
+            short = "rocBLAS " + short[:40] + "..."
         lines.append(f"{short:52s} {str(grid):>20s} {len(d):7d} {sum(d) / len(d):9.2f} {min(d):9.2f} {max(d):9.2f}")
     return "\n".join(lines)
 
