@@ -322,10 +322,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             }
         };
 
+        // Straight-line body: a tile past w1 (the second of the last pair) is
+        // processed fully masked (its rows are clamped loads, its scores -inf,
+        // so p = 0). A `break` here would give the compiler a path on which
+        // tile b's loads are the newest, and its load waits would then drain
+        // every tile in flight.
         for (int tb = w0; tb < w1; tb += 16 * NT) {
 #pragma unroll
             for (int b = 0; b < NT; b++) {
-                if (tb + 16 * b >= w1) break;
                 process(tb + 16 * b, kt[b], vt[b]);
                 load_tile(tb + 16 * (b + NT), kt[b], vt[b]);
             }
