@@ -284,7 +284,9 @@ class PicoAttention:
         return x
 
     def qkv_project_batch(self, layer: int, xb):
-        """q, k, v [n_tok][...] of a prompt (fp32 GEMMs over exactly dequantized weights)."""
+        """q, k, v [n_tok][...] of a prompt: one GEMM over exactly dequantized
+        weights, split into fp16 hi + lo parts with fp32 accumulation (within
+        (3 n_embd + 12) 2^-24 sum |w x| of the reference)."""
         import torch
         n_tok = xb.shape[0]
         dev = xb.device

@@ -3,13 +3,22 @@
 // all tokens, feeding the MFMA prefill.
 //
 // Each GGUF matrix is first dequantized into an fp32 workspace by the
-// expressions of dequantize_row_* (cpp/quant.hpp:176-281), exactly, then
-// Y[n_tok][rows] = X[n_tok][n] W^T runs as a plain fp32 GEMM (rocBLAS sgemm on
-// the context stream), then the bias is added (vec_add: out + b). The weights
-// and the inputs are exact; only the summation order of each dot product
-// differs from the reference's, so q/k/v agree to fp32 rounding (about 1e-6
-// relative) rather than bit for bit. pqa_qkv_project keeps the reference's
-// order for one token.
+// expressions of dequantize_row_* (cpp/quant.hpp:176-281), exactly. Then
+// Y[n_tok][rows] = X[n_tok][n] W^T runs on the fp16 MFMA path with fp32
+// accumulation, as one GEMM over a K of 3n:
+//   every row a of W and of X is scaled by a power of two 2^s (exact) so that
+//   max |a 2^s| lies in [2^14, 2^15), and split into hi = fp16(a 2^s) and
+//   lo = fp16(a 2^s - hi), which carry 22 of its 24 significand bits;
+//   W' = [hi | hi | lo] and X' = [hi | lo | hi] (each 3n halfs per row), so
+//   W' . X' = w_hi x_hi + w_hi x_lo + w_lo x_hi, dropping w_lo x_lo (about
+//   2^-22 of |w x|); fp16 products are exact in fp32;
+//   the result is scaled back by 2^-(s_w + s_x) (exact), then the bias is
+//   added (vec_add: out + b).
+// The error stays within (3n + 12) 2^-24 sum |w x| for any summation order
+// the GEMM takes, so q/k/v agree with the reference to fp32 rounding (about
+// 1e-6 relative) rather than bit for bit. pqa_qkv_project keeps the
+// reference's order for one token.
+#include <hip/hip_fp16.h>
 #include <rocblas/rocblas.h>
 
 #include <string>
@@ -76,13 +85,67 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     }
 }
 
-// out[t][r] = out[t][r] + b[r] (vec_add, cpp/tensor.hpp:410-420)
-__global__ __launch_bounds__(256) void add_bias_kernel(float* out, const uint8_t* b, int btype, int rows, int n_tok) {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long long)rows * n_tok) return;
-    const int r = (int)(i % rows);
-    const float bv = btype == GG_F32 ? ((const float*)b)[r] : bh2f(bld16(b + 2 * r));
-    out[i] = out[i] + bv;
+// One workgroup per row of n floats: max |a| over the row, the power of two
+// 2^s that takes it into [2^14, 2^15), dst row = the hi/lo halves of a 2^s in
+// the order [hi | hi | lo] (weights) or [hi | lo | hi] (inputs), and
+// inv_scale[row] = 2^-s.
+__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ src, int n, _Float16* __restrict__ dst,
+                                                     float* __restrict__ inv_scale, int x_layout) {
+    __shared__ float s_max[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* a = src + (size_t)row * n;
+    _Float16* d = dst + (size_t)row * 3 * n;
+    float mx = 0.0f;
+    for (int i = tid; i < n; i += 256) mx = fmaxf(mx, fabsf(a[i]));
+    mx = group_max<64>(mx);
+    if ((tid & 63) == 0) s_max[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    // mx in [2^e, 2^(e+1)): s = 14 - e; an all-zero row keeps s = 0
+    const int s = mx > 0.0f ? min(126, max(-126, 14 - ilogbf(mx))) : 0;
+    const float sc = ldexpf(1.0f, s);
+    if (tid == 0) inv_scale[row] = ldexpf(1.0f, -s);
+    for (int i = tid; i < n; i += 256) {
+        const float v = a[i] * sc;
+        const _Float16 hi = (_Float16)v;
+        const _Float16 lo = (_Float16)(v - (float)hi);
+        d[i] = hi;
+        d[n + i] = x_layout ? lo : hi;
+        d[2 * n + i] = x_layout ? hi : lo;
+    }
+}
+
+// The three outputs of the batched GEMM and their biases.
+struct ScatterArgs {
+    float* out[3];
+    const uint8_t* b[3];
+    int btype[3];
+    int rows[3];
+};
+
+// Y [n_tok][total] holds q|k|v of every token scaled by 2^(s_w + s_x):
+// out_m[t][r] = Y[t][off_m + r] * 2^-(s_w + s_x), an exact rescale, then
+// out + b[r] (vec_add, cpp/tensor.hpp:410-420). Thread: 4 consecutive rows of
+// one token (rows of q and kv are multiples of 4).
+__global__ __launch_bounds__(256) void unscale_scatter_kernel(const float* __restrict__ Y, int total,
+                                                              const float* __restrict__ w_inv,
+                                                              const float* __restrict__ x_inv, const ScatterArgs a) {
+    const int t = blockIdx.y;
+    const int r = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (r >= total) return;
+    const int m = r < a.rows[0] ? 0 : (r < a.rows[0] + a.rows[1] ? 1 : 2);
+    const int rr = r - (m > 0 ? a.rows[0] : 0) - (m > 1 ? a.rows[1] : 0);
+    const floatx4 y = *(const floatx4*)(Y + (size_t)t * total + r);
+    const floatx4 wi = *(const floatx4*)(w_inv + r);
+    const float xi = x_inv[t];
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float v = y[e] * (wi[e] * xi);
+        if (a.b[m]) v = v + (a.btype[m] == GG_F32 ? ((const float*)a.b[m])[rr + e] : bh2f(bld16(a.b[m] + 2 * (rr + e))));
+        o[e] = v;
+    }
+    *(floatx4*)(a.out[m] + (size_t)t * a.rows[m] + rr) = o;
 }
 
 static hipError_t launch_dequant(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s) {
@@ -131,6 +194,69 @@ void pqa_free_batch(pqa_ctx* c) {
     c->blas = nullptr;
     if (c->wf32) (void)hipFree(c->wf32);
     c->wf32 = nullptr;
+    if (c->bsplit) (void)hipFree(c->bsplit);
+    c->bsplit = nullptr;
+    c->bsplit_bytes = 0;
+}
+
+static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// A layer's W' = [hi | hi | lo] rows of attn_q, attn_k and attn_v, one after
+// the other ([total][3n] halfs), then their inverse scales: made once, on the
+// first batched call for the layer (dequantized through the fp32 workspace).
+static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
+    auto& p = ctx->proj[layer];
+    if (p.split) return PQA_OK;
+    const int n = p.n_embd;
+    const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
+    const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
+    const size_t wb = up256(total * 3 * n * 2);
+    if (int rc = ensure_batch(ctx, ctx->q_dim * (size_t)n, fn)) return rc;
+    void* buf = nullptr;
+    if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256(total * 4)), fn)) return rc;
+    _Float16* w3 = (_Float16*)buf;
+    float* w_inv = (float*)((char*)buf + wb);
+    size_t off = 0;
+    for (int i = 0; i < 3; i++) {
+        hipError_t e = pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(pqa::split3_kernel, dim3(rows[i]), dim3(256), 0, ctx->stream, (const float*)ctx->wf32, n,
+                               w3 + off * 3 * n, w_inv + off, 0);
+            e = hipGetLastError();
+        }
+        if (int rc = hip_check(ctx, e, fn)) {
+            (void)hipFree(buf);
+            return rc;
+        }
+        off += rows[i];
+    }
+    p.split = buf;
+    return PQA_OK;
+}
+
+// Per call: X' [n_tok][3n] halfs, the inverse scales of X's rows, and the
+// GEMM result Y [n_tok][total] floats.
+struct SplitBufs {
+    _Float16* x3;
+    float* x_inv;
+    float* y;
+};
+
+static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs* sb, const char* fn) {
+    const size_t xb = up256((size_t)n_tok * 3 * n * 2), xs = up256((size_t)n_tok * 4);
+    const size_t need = xb + xs + (size_t)n_tok * total * 4;
+    if (need > ctx->bsplit_bytes) {
+        if (ctx->bsplit) (void)hipFree(ctx->bsplit);
+        ctx->bsplit = nullptr;
+        ctx->bsplit_bytes = 0;
+        if (int rc = hip_check(ctx, hipMalloc(&ctx->bsplit, need), fn)) return rc;
+        ctx->bsplit_bytes = need;
+    }
+    char* base = (char*)ctx->bsplit;
+    sb->x3 = (_Float16*)base;
+    sb->x_inv = (float*)(base + xb);
+    sb->y = (float*)(base + xb + xs);
+    return PQA_OK;
 }
 
 extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k,
@@ -141,29 +267,36 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
     if (ctx->proj.empty() || !ctx->proj[layer].n_embd)
         return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: no projection weights for this layer");
     if (n_tok <= 0 || !xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: bad arguments");
+    const int n = ctx->proj[layer].n_embd;
+    if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
-    const int n = p.n_embd;
-    const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
-    float* outs[3] = {q, k, v};
-    if (int rc = ensure_batch(ctx, (size_t)ctx->q_dim * n, fn)) return rc;
+    const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
+    const _Float16* w3 = (const _Float16*)p.split;
+    const float* w_inv = (const float*)((const char*)p.split + up256(total * 3 * n * 2));
+    SplitBufs sb;
+    if (int rc = ensure_split(ctx, n_tok, n, total, &sb, fn)) return rc;
+    hipLaunchKernelGGL(pqa::split3_kernel, dim3(n_tok), dim3(256), 0, ctx->stream, xb, n, sb.x3, sb.x_inv, 1);
+    if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
+    // row-major Y[n_tok][total] = X'[n_tok][3n] W'[total][3n]^T, i.e.
+    // column-major C (total x n_tok) = W'^T (total x 3n) * X'^T (3n x n_tok)
     const float one = 1.0f, zero = 0.0f;
+    if (rocblas_gemm_ex((rocblas_handle)ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (int)total, n_tok,
+                        3 * n, &one, w3, rocblas_datatype_f16_r, 3 * n, sb.x3, rocblas_datatype_f16_r, 3 * n, &zero,
+                        sb.y, rocblas_datatype_f32_r, (int)total, sb.y, rocblas_datatype_f32_r, (int)total,
+                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0) != rocblas_status_success)
+        return set_err(ctx, PQA_ERR_HIP, "pqa_qkv_project_batch: rocblas_gemm_ex failed");
+    pqa::ScatterArgs sa;
+    float* outs[3] = {q, k, v};
     for (int i = 0; i < 3; i++) {
-        if (int rc = hip_check(ctx, pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream),
-                               fn))
-            return rc;
-        // row-major Y[n_tok][rows] = X[n_tok][n] W[rows][n]^T, i.e. column-major
-        // C (rows x n_tok) = W^T (rows x n) * X^T (n x n_tok)
-        if (rocblas_sgemm((rocblas_handle)ctx->blas, rocblas_operation_transpose, rocblas_operation_none, rows[i],
-                          n_tok, n, &one, ctx->wf32, n, xb, n, &zero, outs[i], rows[i]) != rocblas_status_success)
-            return set_err(ctx, PQA_ERR_HIP, "pqa_qkv_project_batch: rocblas_sgemm failed");
-        if (p.b[i]) {
-            const long long items = (long long)rows[i] * n_tok;
-            hipLaunchKernelGGL(pqa::add_bias_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, ctx->stream,
-                               outs[i], (const uint8_t*)p.b[i], p.btype[i], rows[i], n_tok);
-            if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
-        }
+        sa.out[i] = outs[i];
+        sa.b[i] = (const uint8_t*)p.b[i];
+        sa.btype[i] = p.btype[i];
+        sa.rows[i] = i == 0 ? (int)ctx->q_dim : (int)ctx->kv_dim;
     }
-    return PQA_OK;
+    const unsigned gx = (unsigned)((total / 4 + 255) / 256);
+    hipLaunchKernelGGL(pqa::unscale_scatter_kernel, dim3(gx, n_tok), dim3(256), 0, ctx->stream, (const float*)sb.y,
+                       (int)total, w_inv, (const float*)sb.x_inv, sa);
+    return hip_check(ctx, hipGetLastError(), fn);
 }
 
 extern "C" int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* out) {

@@ -24,6 +24,9 @@ struct pqa_proj_weights {
     int wtype[4] = {0, 0, 0, 0}, btype[4] = {0, 0, 0, 0}, stride[4] = {0, 0, 0, 0};
     int n_embd = 0;   // q/k/v set (row width); 0: not set
     int out_rows = 0; // attn_output set (its row count, = n_embd); 0: not set
+    // the batched path's fp16 hi/lo copy of the attn_q, attn_k and attn_v rows
+    // and their row scales; made on the first batched call, dropped with the weights
+    void* split = nullptr;
 };
 
 struct pqa_ctx {
@@ -62,6 +65,8 @@ struct pqa_ctx {
     size_t wf32_floats = 0;
     float* bqkv = nullptr;
     size_t bqkv_floats = 0;
+    void* bsplit = nullptr;  // fp16 hi/lo operands of the batched GEMMs and their row scales
+    size_t bsplit_bytes = 0;
 
     // staging for the _host entry points
     float* stage = nullptr;

@@ -404,6 +404,8 @@ void free_proj(pqa_ctx* c, int layer) {
     }
     p.n_embd = 0;
     p.out_rows = 0;
+    if (p.split) (void)hipFree(p.split);
+    p.split = nullptr;
 }
 
 }  // namespace
@@ -468,6 +470,8 @@ extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
     if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
     auto& p = ctx->proj[layer];
     for (int i = 0; i < 3; i++) free_matrix(p, i);
+    if (p.split) (void)hipFree(p.split);  // the batched path's copy of the old rows
+    p.split = nullptr;
     p.n_embd = 0;
     for (int i = 0; i < 3; i++)
         if (int rc = upload_matrix(ctx, p, i, fn, n_embd, rows[i], w[i], wt[i], b[i], bt[i])) {

@@ -192,10 +192,12 @@ def test_attention_block_from_xb_to_residual():
 
 
 def test_batched_projection_within_fp32_reordering_bound():
-    # Qwen3-4B widths, 37 tokens: the weights are dequantized exactly, only
-    # the order of each dot product's sum differs, so |got - ref| <=
-    # 2 (n + 1) 2^-24 sum_i |w_i x_i| (product rounding and any summation
-    # order, both sides)
+    # Qwen3-4B widths, 37 tokens: the weights are dequantized exactly; the
+    # batched path splits w and x (scaled by powers of two) into fp16 hi + lo
+    # and sums w_hi x_hi + w_hi x_lo + w_lo x_hi in fp32 over 3n terms in the
+    # GEMM's own order. Its error is at most (3n + 12) 2^-24 sum_i |w_i x_i|
+    # (2^-22 per product for the split, any summation order over 3n terms);
+    # the reference's sequential sums add (n + 1) 2^-24 sum_i |w_i x_i|
     print("batched projection", flush=True)
     rng = np.random.default_rng(31337)
     nh, nkv, hd, dim, n_tok = 32, 8, 128, 2560, 37
@@ -213,9 +215,34 @@ def test_batched_projection_within_fp32_reordering_bound():
         wf = np.stack([O.dequant_row(wt, w[r], dim) for r in range(rows)]).astype(np.float64)
         for t in range(0, n_tok, 6):
             want = O.matmul_bias(x[t], w, wt, rows, b, bt)
-            bound = 2.0 * (dim + 1) * 2.0 ** -24 * (np.abs(wf) @ np.abs(x[t].astype(np.float64))) + 1e-30
+            mag = np.abs(wf) @ np.abs(x[t].astype(np.float64))
+            bound = (4 * dim + 13) * 2.0 ** -24 * mag + 1e-30
             err = np.abs(g[t].astype(np.float64) - want)
             assert np.all(err <= bound), (name, t, float(np.max(err / bound)))
+            # and in practice far inside it: a typical error of a few ulps of sum |w x|
+            assert float(np.median(err / (mag + 1e-30))) < 64 * 2.0 ** -24, (name, t)
+    att.close()
+
+
+def test_batched_projection_follows_replaced_weights():
+    # the batched path keeps a split copy of a layer's rows; replacing the
+    # layer's weights must drop it
+    print("batched projection after new weights", flush=True)
+    rng = np.random.default_rng(4242)
+    nh, nkv, hd, dim, n_tok = 4, 2, 64, 512, 9
+    att = PicoAttention(2, 16, nh, nkv, hd)
+    x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    xd = torch.from_numpy(x).to(torch.device("cuda:0"))
+    for rep in range(2):
+        ws = [make_rows(rng, O.GGUF_Q8_0, rows, dim) for rows in (nh * hd, nkv * hd, nkv * hd)]
+        att.set_qkv_weights(1, dim, ws[0], O.GGUF_Q8_0, ws[1], O.GGUF_Q8_0, ws[2], O.GGUF_Q8_0)
+        got = [g.cpu().numpy() for g in att.qkv_project_batch(1, xd)]
+        for g, w in zip(got, ws):
+            wf = np.stack([O.dequant_row(O.GGUF_Q8_0, w[r], dim) for r in range(w.shape[0])]).astype(np.float64)
+            for t in range(n_tok):
+                want = O.matmul_bias(x[t], w, O.GGUF_Q8_0, w.shape[0])
+                mag = np.abs(wf) @ np.abs(x[t].astype(np.float64))
+                assert np.all(np.abs(g[t] - want) <= (4 * dim + 13) * 2.0 ** -24 * mag + 1e-30), (rep, t)
     att.close()
 
 
