@@ -224,6 +224,31 @@ def test_batched_projection_within_fp32_reordering_bound():
     att.close()
 
 
+@pytest.mark.parametrize("wtype", TYPES)
+def test_batched_projection_every_type(wtype):
+    # the batched path over each weight type the reference dequantizes, odd
+    # token counts, F32 and F16 biases; same bound as above
+    print(f"batched projection type {wtype}", flush=True)
+    rng = np.random.default_rng(900 + wtype)
+    nh, nkv, hd, dim = 4, 2, 64, 1024  # whole blocks of every type (Q6_K rows: multiples of 512)
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    mats = [(make_rows(rng, wtype, rows, dim, special=True), make_bias(rng, bt, rows) if bt else None, bt)
+            for rows, bt in ((nh * hd, O.GGUF_F16), (nkv * hd, O.GGUF_NONE), (nkv * hd, O.GGUF_F32))]
+    att.set_qkv_weights(0, dim, mats[0][0], wtype, mats[1][0], wtype, mats[2][0], wtype,
+                        mats[0][1], mats[0][2], None, 0, mats[2][1], mats[2][2])
+    for n_tok in (1, 5):
+        x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+        got = [g.cpu().numpy() for g in att.qkv_project_batch(0, torch.from_numpy(x).to(torch.device("cuda:0")))]
+        for name, g, (w, b, bt) in zip("qkv", got, mats):
+            wf = np.stack([O.dequant_row(wtype, w[r], dim) for r in range(w.shape[0])]).astype(np.float64)
+            for t in range(n_tok):
+                want = O.matmul_bias(x[t], w, wtype, w.shape[0], b, bt)
+                mag = np.abs(wf) @ np.abs(x[t].astype(np.float64))
+                err = np.abs(g[t].astype(np.float64) - want)
+                assert np.all(err <= (4 * dim + 13) * 2.0 ** -24 * mag + 1e-30), (name, n_tok, t)
+    att.close()
+
+
 def test_batched_projection_follows_replaced_weights():
     # the batched path keeps a split copy of a layer's rows; replacing the
     # layer's weights must drop it
