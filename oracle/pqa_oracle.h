@@ -25,6 +25,13 @@
  *                         float64 brute-force softmax; ctx=1, equal-key and
  *                         dominant-key closed forms
  *   rng                   SplitMix64 published test vector; N(0,1) moments
+ *   projections           the reference's own dequantize_row, vec_dot and
+ *                         matmul_bias compiled from its sources (bit-exact);
+ *                         closed forms per GGUF type; a summation-order case
+ *                         that only the reference's order passes
+ *   .kvc format           (oracle/__init__.py) the reference's compiled
+ *                         kvcache_save / kvcache_load: identical files and
+ *                         cache bytes, short and malformed files included
  */
 #ifndef PQA_ORACLE_H
 #define PQA_ORACLE_H
