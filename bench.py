@@ -28,6 +28,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 import argparse
 import ctypes as C
 import json
+import re
 import os
 import sys
 import time
@@ -528,6 +529,9 @@ def summarize_trace(trace_dir):
     groups = {}
     for r in _rows(_find(trace_dir, "kernel_trace.csv")):
         name = r["Kernel_Name"]
+        m = re.match(r"_ZN3pqa(\d+)", name)  # a name the tracer left mangled: pqa::<identifier>
+        if m:
+            name = "pqa::" + name[m.end():m.end() + int(m.group(1))]
         # this library's kernels, and rocBLAS's GEMM kernels of the batched projections
         if not name.startswith(("void pqa::", "pqa::", "Cijk_")):
             continue
