@@ -373,11 +373,13 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
     return res
 
 
-def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, s=2048, steps=3, warmup=1):
+def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, s=2048, steps=3, warmup=1, cpu=True):
     """The prompt path of a Qwen3-4B-shaped layer from the normed inputs
     (pqa_prefill_x): exact dequantization of Q4_K attn_q/attn_k and Q6_K
-    attn_v, three fp32 GEMMs over 2048 tokens (rocBLAS), bias, then the
-    K/V append and the causal MFMA prefill; 36 layers per step."""
+    attn_v, split into fp16 hi/lo parts (kept per layer after the first
+    call), one GEMM over 2048 tokens (rocBLAS, fp16 MFMA with fp32
+    accumulation), bias, then the K/V append and the causal MFMA prefill; 36
+    layers per step."""
     Q4K, Q6K = 13, 15
     cx = Ctx(n_layers, s, nh, nkv, hd, 0, 1e6)
     rng = np.random.default_rng(909)
@@ -385,6 +387,8 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
     vp = lambda a: a.ctypes.data_as(C.c_void_p)
     for layer in range(n_layers):
         wq, wk, wv = gguf_rows(rng, Q4K, nh * hd, dim), gguf_rows(rng, Q4K, nkv * hd, dim), gguf_rows(rng, Q6K, nkv * hd, dim)
+        if layer == 0:
+            w0 = (wq, wk, wv)
         cx.check(cx.L.pqa_set_qkv_weights(cx.h, layer, dim, vp(wq), Q4K, None, 0, vp(wk), Q4K, None, 0, vp(wv), Q6K,
                                           None, 0), cx.h)
     x = torch.from_numpy(rng.standard_normal((s, dim), dtype=np.float32)).to(dev)
@@ -406,6 +410,22 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
            "us_per_layer": round(us, 1), "projection_GFLOP_per_layer": round(gemm_flops / 1e9, 1),
            "attention_GFLOP_per_layer": round(attn_flops / 1e9, 1),
            "TFLOP_per_s_total": round((gemm_flops + attn_flops) / (us * 1e-6) / 1e12, 1)}
+    if cpu:
+        import oracle as O
+        if O.RefModel.available("B"):
+            # the reference's per-token matmul_bias (forward_batch's projections)
+            # for a few tokens of layer 0, scaled to the prompt; the attention
+            # part of the reference's prompt path is not in this figure
+            ref = O.RefProj("B")
+            xh = x[:4].cpu().numpy()
+            t0 = time.perf_counter()
+            for t in range(4):
+                for w, wt in zip(w0, (Q4K, Q4K, Q6K)):
+                    ref.matmul_bias(xh[t], w, wt, w.shape[0])
+            per_tok = (time.perf_counter() - t0) / 4
+            res["cpu_baseline"] = {"kind": "reference", "cores": 1, "us_per_layer_projections": round(per_tok * s * 1e6),
+                                   "sample": f"TensorOps::matmul_bias of the reference (build B) for q/k/v of 4 "
+                                             f"tokens of layer 0, scaled to {s} tokens; projections only"}
     log(f"[bench] prefill from xb: {us:.1f} us/layer; {res}")
     return res
 
@@ -630,7 +650,7 @@ def main():
         workloads["qwen3_8b_kvc_save_load"] = kvc_workload(torch, dev)
         workloads["qwen3_8b_qkv_proj"] = proj_workload(torch, dev, steps=args.steps, warmup=args.warmup,
                                                        cpu=not args.no_cpu)
-        workloads["qwen3_4b_prefill_from_xb"] = prefill_x_workload(torch, dev)
+        workloads["qwen3_4b_prefill_from_xb"] = prefill_x_workload(torch, dev, cpu=not args.no_cpu)
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]
