@@ -259,32 +259,49 @@ static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs*
     return PQA_OK;
 }
 
-extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k,
-                                     float* v) {
-    static const char* fn = "pqa_qkv_project_batch";
-    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_qkv_project_batch: ctx is NULL");
-    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: bad layer");
-    if (ctx->proj.empty() || !ctx->proj[layer].n_embd)
-        return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: no projection weights for this layer");
-    if (n_tok <= 0 || !xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: bad arguments");
+// X' and the GEMM of one call: sb->y [n_tok][q_dim + 2 kv_dim] = X W^T, every
+// element scaled by 2^(s_w[c] + s_x[t]); *w_inv = the inverse column scales.
+static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, SplitBufs* sb, const float** w_inv,
+                      const char* fn) {
     const int n = ctx->proj[layer].n_embd;
     if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
     const _Float16* w3 = (const _Float16*)p.split;
-    const float* w_inv = (const float*)((const char*)p.split + up256(total * 3 * n * 2));
-    SplitBufs sb;
-    if (int rc = ensure_split(ctx, n_tok, n, total, &sb, fn)) return rc;
-    hipLaunchKernelGGL(pqa::split3_kernel, dim3(n_tok), dim3(256), 0, ctx->stream, xb, n, sb.x3, sb.x_inv, 1);
+    *w_inv = (const float*)((const char*)p.split + up256(total * 3 * n * 2));
+    if (int rc = ensure_split(ctx, n_tok, n, total, sb, fn)) return rc;
+    hipLaunchKernelGGL(pqa::split3_kernel, dim3(n_tok), dim3(256), 0, ctx->stream, xb, n, sb->x3, sb->x_inv, 1);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
     // row-major Y[n_tok][total] = X'[n_tok][3n] W'[total][3n]^T, i.e.
     // column-major C (total x n_tok) = W'^T (total x 3n) * X'^T (3n x n_tok)
     const float one = 1.0f, zero = 0.0f;
     if (rocblas_gemm_ex((rocblas_handle)ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (int)total, n_tok,
-                        3 * n, &one, w3, rocblas_datatype_f16_r, 3 * n, sb.x3, rocblas_datatype_f16_r, 3 * n, &zero,
-                        sb.y, rocblas_datatype_f32_r, (int)total, sb.y, rocblas_datatype_f32_r, (int)total,
+                        3 * n, &one, w3, rocblas_datatype_f16_r, 3 * n, sb->x3, rocblas_datatype_f16_r, 3 * n, &zero,
+                        sb->y, rocblas_datatype_f32_r, (int)total, sb->y, rocblas_datatype_f32_r, (int)total,
                         rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0) != rocblas_status_success)
-        return set_err(ctx, PQA_ERR_HIP, "pqa_qkv_project_batch: rocblas_gemm_ex failed");
+        return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": rocblas_gemm_ex failed");
+    return PQA_OK;
+}
+
+static int check_batch(pqa_ctx* ctx, int layer, int n_tok, const char* fn) {
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": bad layer");
+    if (ctx->proj.empty() || !ctx->proj[layer].n_embd)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": no projection weights for this layer");
+    if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": n_tok must be positive");
+    return PQA_OK;
+}
+
+extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k,
+                                     float* v) {
+    static const char* fn = "pqa_qkv_project_batch";
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_qkv_project_batch: ctx is NULL");
+    if (int rc = check_batch(ctx, layer, n_tok, fn)) return rc;
+    if (!xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: NULL buffer");
+    SplitBufs sb;
+    const float* w_inv = nullptr;
+    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn)) return rc;
+    const auto& p = ctx->proj[layer];
+    const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
     pqa::ScatterArgs sa;
     float* outs[3] = {q, k, v};
     for (int i = 0; i < 3; i++) {
@@ -299,23 +316,29 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
     return hip_check(ctx, hipGetLastError(), fn);
 }
 
+// The prompt path from the normed inputs: the GEMM result goes to the prefill
+// kernels as it is (they undo the scales and add the biases as they read q, k
+// and v), without a q/k/v copy.
 extern "C" int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* out) {
     static const char* fn = "pqa_prefill_x";
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_prefill_x: ctx is NULL");
-    if (n_tok <= 0 || !xb || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_x: bad arguments");
+    if (int rc = check_batch(ctx, layer, n_tok, fn)) return rc;
+    if (!xb || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_x: NULL buffer");
+    if (((uintptr_t)out & 15) != 0) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_x: out must be 16-byte aligned");
     if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill_x: positions past max_seq_len");
-    const size_t need = (size_t)n_tok * (ctx->q_dim + 2 * ctx->kv_dim);
-    if (need > ctx->bqkv_floats) {
-        if (ctx->bqkv) (void)hipFree(ctx->bqkv);
-        ctx->bqkv = nullptr;
-        ctx->bqkv_floats = 0;
-        if (int rc = hip_check(ctx, hipMalloc(&ctx->bqkv, need * 4), fn)) return rc;
-        ctx->bqkv_floats = need;
+    SplitBufs sb;
+    const float* w_inv = nullptr;
+    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn)) return rc;
+    const auto& p = ctx->proj[layer];
+    pqa::PrefillScaled ys;
+    ys.y = sb.y;
+    ys.ld = (int)(ctx->q_dim + 2 * ctx->kv_dim);
+    ys.w_inv = w_inv;
+    ys.x_inv = sb.x_inv;
+    for (int i = 0; i < 3; i++) {
+        ys.b[i] = (const uint8_t*)p.b[i];
+        ys.bt[i] = p.btype[i];
     }
-    float* q = ctx->bqkv;
-    float* k = q + (size_t)n_tok * ctx->q_dim;
-    float* v = k + (size_t)n_tok * ctx->kv_dim;
-    if (int rc = pqa_qkv_project_batch(ctx, layer, n_tok, xb, q, k, v)) return rc;
-    return pqa_prefill(ctx, layer, start_pos, n_tok, q, k, v, out);
+    return hip_check(ctx, pqa::launch_prefill_scaled(ctx, layer, start_pos, n_tok, ys, out), fn);
 }

@@ -52,19 +52,20 @@ struct pqa_ctx {
     int cu_count = 256;
 
     // prefill: q = fp16 hi + lo in the score products (outlier-heavy caches)
-    int prefill_split_q = 0;
+    // -1 (default): q as fp16 hi + lo in layers without QK-norm (their q and k
+    // are unbounded), one fp16 q in layers with it; 0 / 1: that mode everywhere
+    int prefill_split_q = -1;
 
     // projections (pqa_set_qkv_weights) and the q/k/v of pqa_decode_x
     std::vector<pqa_proj_weights> proj;
     float* qkv = nullptr;  // [q_dim + 2 kv_dim + q_dim]: q, k, v and the attention output
 
     // batched projections (pqa_batch.hip): rocBLAS handle, fp32 weights of one
-    // matrix, q/k/v of pqa_prefill_x; made on first use
+    // matrix while a layer's split copy is made, and the per-call operands;
+    // made on first use
     void* blas = nullptr;
     float* wf32 = nullptr;
     size_t wf32_floats = 0;
-    float* bqkv = nullptr;
-    size_t bqkv_floats = 0;
     void* bsplit = nullptr;  // fp16 hi/lo operands of the batched GEMMs and their row scales
     size_t bsplit_bytes = 0;
 
@@ -95,6 +96,18 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
                          const float* v, float* out);
 hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
                           const float* k, const float* v, float* out);
+// q/k/v of a prompt as the columns of one GEMM result y [n_tok][ld] (q at
+// column 0, k at q_dim, v at q_dim + kv_dim), scaled by powers of two: the
+// value of column c of token t is y * (w_inv[c] * x_inv[t]) + b_m[c]
+struct PrefillScaled {
+    const float* y;
+    int ld;
+    const float* w_inv;
+    const float* x_inv;
+    const uint8_t* b[3];  // q, k, v biases or null
+    int bt[3];
+};
+hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, const PrefillScaled& ys, float* out);
 hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
 hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
 hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);

@@ -33,7 +33,7 @@
 namespace pqa {
 
 struct KvArgs {
-    const float* k;  // [n_tok][kv_dim]
+    const float* k;  // row of token t at k + t * ld
     const float* v;
     const float* kn;       // [HD] or null
     const float* wpad;     // 2*HD readable floats, loaded in place of absent norm weights
@@ -42,11 +42,32 @@ struct KvArgs {
     uint16_t* kc;  // layer slice [S][kv_dim]
     uint16_t* vc;
     int start, n_tok, nkv, rope;
+    int ld;  // floats between the k (and v) rows of consecutive tokens
+    // scaled inputs (YS): k = k * (kw[c] * x_inv[t]) + kb[c] for column c of
+    // token t, v likewise; kb / vb may be null
+    const float* kw;
+    const float* vw;
+    const float* x_inv;
+    const uint8_t* kb;
+    const uint8_t* vb;
+    int kbt, vbt;
 };
+
+// y * (w * xi) + b[c .. c+3] (an exact power-of-two rescale, then vec_add,
+// cpp/tensor.hpp:410-420), for 4 consecutive columns c of one token
+__device__ __forceinline__ float bias_at(const uint8_t* b, int bt, int c) {
+    return bt == GG_F32 ? ((const float*)b)[c] : f16_bits_to_f32(((const uint16_t*)b)[c]);
+}
+__device__ __forceinline__ float4 unscale4(float4 y, float4 w, float xi, const uint8_t* b, int bt, int c) {
+    float4 r = float4{y.x * (w.x * xi), y.y * (w.y * xi), y.z * (w.z * xi), y.w * (w.w * xi)};
+    if (b) r = float4{r.x + bias_at(b, bt, c), r.y + bias_at(b, bt, c + 1), r.z + bias_at(b, bt, c + 2),
+                      r.w + bias_at(b, bt, c + 3)};
+    return r;
+}
 
 constexpr int kKvThreads = 256;
 
-template <int HD>
+template <int HD, bool YS>
 __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) {
     constexpr int H4 = HD / 4;
     constexpr int IPW = 64 / H4;  // rows per wave
@@ -62,8 +83,14 @@ __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) 
     const int tok = it / a.nkv, kvh = it - tok * a.nkv;
     const int pos = a.start + tok;
     const size_t kv_dim = (size_t)a.nkv * HD;
-    const float4 kx = ((const float4*)(a.k + (size_t)tok * kv_dim + (size_t)kvh * HD))[t];
-    const float4 vx = ((const float4*)(a.v + (size_t)tok * kv_dim + (size_t)kvh * HD))[t];
+    float4 kx = ((const float4*)(a.k + (size_t)tok * a.ld + (size_t)kvh * HD))[t];
+    float4 vx = ((const float4*)(a.v + (size_t)tok * a.ld + (size_t)kvh * HD))[t];
+    if constexpr (YS) {
+        const float xi = a.x_inv[tok];
+        const int c = kvh * HD + 4 * t;
+        kx = unscale4(kx, ((const float4*)(a.kw + (size_t)kvh * HD))[t], xi, a.kb, a.kbt, c);
+        vx = unscale4(vx, ((const float4*)(a.vw + (size_t)kvh * HD))[t], xi, a.vb, a.vbt, c);
+    }
     const float4 wk = ((const float4*)(a.kn ? a.kn : a.wpad + HD))[t];
     const int ci = rope_angle_f4<HD>(a.rope, t);
     const float4 cs = ((const float4*)(a.cos_tab + (size_t)pos * (HD / 2)))[ci];
@@ -91,7 +118,7 @@ __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) 
 }
 
 struct AttnArgs {
-    const float* q;   // [n_tok][nh*HD] fp32 projections
+    const float* q;   // fp32 projections: row of token t at q + t * q_ld, heads one after the other
     const float* qn;  // [HD] or null
     const float* wpad;
     const float* cos_tab;  // [S][HD/2]
@@ -101,6 +128,12 @@ struct AttnArgs {
     float* out;
     int start, n_tok, nh, g, n_kv, kv_dim, rows, nblk, rope;
     float qscale;
+    int q_ld;  // floats between the q rows of consecutive tokens
+    // scaled q (YS): q = q * (qw[c] * x_inv[t]) + qb[c] for column c of token t
+    const float* qw;
+    const float* x_inv;
+    const uint8_t* qb;
+    int qbt;
 };
 
 constexpr int kAttnThreads = 512;  // 2 groups of 4 waves: even and odd key tiles
@@ -130,7 +163,7 @@ struct PrefillTile {
 
 // SPLITQ: scores use q = hi + lo (two fp16 MFMAs into one fp32 accumulator),
 // which keeps fp32-level score precision when keys carry large outliers.
-template <int HD, bool SPLITQ>
+template <int HD, bool SPLITQ, bool YS>
 __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const AttnArgs a) {
     using T = PrefillTile<HD>;
     constexpr int QK = HD / 16;  // k-steps of S^T = K Q^T
@@ -261,14 +294,14 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         constexpr int NQ = 32 / RPQ / 2;      // loads per wave (the two waves of a row group split them)
         char* qst = &lds[1][0][0][0] + wr * 32 * HD * 4;
         const int tq0 = min(R0, a.rows - 1) / a.g;  // first token of the row group
-        const char* qbase = (const char*)(a.q + (size_t)tq0 * a.nh * HD);
+        const char* qbase = (const char*)(a.q + (size_t)tq0 * a.q_ld);
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             const int j = par * NQ + i;
             const int rr = j * RPQ + lane / CQ;
             const int Rq = min(R0 + rr, a.rows - 1);
             const int tq = Rq / a.g;
-            const unsigned qoff = (unsigned)((((tq - tq0) * a.nh + kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
+            const unsigned qoff = (unsigned)(((tq - tq0) * a.q_ld + (kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
             const int c = (lane % CQ) ^ (rr & (CQ - 1));
             lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
         }
@@ -291,6 +324,24 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 cf[q] = *(const float4*)(crow + ai);
                 sf[q] = *(const float4*)(srow + ai);
             }
+            // scaled q (YS): the column scales and biases of this lane's dims,
+            // loaded with the RoPE rows so that one wait covers them
+            float4 qwv[YS ? NF : 1], qbv[YS ? NF : 1];
+            float qxi = 1.0f;
+            if constexpr (YS) {
+                const int pRc = min(pR, a.rows - 1);
+                const int ptq = pRc / a.g;
+                const int col0 = (kvh * a.g + (pRc - ptq * a.g)) * HD;
+                qxi = a.x_inv[ptq];
+#pragma unroll
+                for (int i = 0; i < NF; i++) {
+                    const int c = col0 + 4 * pchunk(i);
+                    qwv[i] = *(const float4*)(a.qw + c);
+                    qbv[i] = a.qb ? float4{bias_at(a.qb, a.qbt, c), bias_at(a.qb, a.qbt, c + 1),
+                                           bias_at(a.qb, a.qbt, c + 2), bias_at(a.qb, a.qbt, c + 3)}
+                                  : float4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();  // q rows and s_qw landed
             float x[NF][4];
@@ -299,6 +350,21 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             for (int i = 0; i < NF; i++) {
                 const float4 u = *(const float4*)(rowp + 16 * (pchunk(i) ^ (prow & (CQ - 1))));
                 x[i][0] = u.x, x[i][1] = u.y, x[i][2] = u.z, x[i][3] = u.w;
+            }
+            if constexpr (YS) {  // q = y * (w * xi), then + b (vec_add) when the layer has a bias
+#pragma unroll
+                for (int i = 0; i < NF; i++) {
+                    x[i][0] = x[i][0] * (qwv[i].x * qxi);
+                    x[i][1] = x[i][1] * (qwv[i].y * qxi);
+                    x[i][2] = x[i][2] * (qwv[i].z * qxi);
+                    x[i][3] = x[i][3] * (qwv[i].w * qxi);
+                    if (a.qb) {
+                        x[i][0] = x[i][0] + qbv[i].x;
+                        x[i][1] = x[i][1] + qbv[i].y;
+                        x[i][2] = x[i][2] + qbv[i].z;
+                        x[i][3] = x[i][3] + qbv[i].w;
+                    }
+                }
             }
             if (a.qn) {
                 float ss = 0.0f;
@@ -562,9 +628,9 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
     }
 }
 
-template <int HD>
+template <int HD, bool YS>
 static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
-                                    const float* k, const float* v, float* out) {
+                                    const float* k, const float* v, float* out, const PrefillScaled* ys) {
     const bool norm = ctx->has_qk_norm[layer] != 0;
     const float* qn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD : nullptr;
     const float* kn = norm ? ctx->qk_norm + (size_t)layer * 2 * HD + HD : nullptr;
@@ -584,9 +650,25 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     p.n_tok = n_tok;
     p.nkv = ctx->n_kv_heads;
     p.rope = ctx->rope_style;
+    p.ld = (int)ctx->kv_dim;
+    p.kw = p.vw = p.x_inv = nullptr;
+    p.kb = p.vb = nullptr;
+    p.kbt = p.vbt = 0;
+    if (YS) {
+        p.k = ys->y + ctx->q_dim;
+        p.v = ys->y + ctx->q_dim + ctx->kv_dim;
+        p.ld = ys->ld;
+        p.kw = ys->w_inv + ctx->q_dim;
+        p.vw = ys->w_inv + ctx->q_dim + ctx->kv_dim;
+        p.x_inv = ys->x_inv;
+        p.kb = ys->b[1];
+        p.kbt = ys->bt[1];
+        p.vb = ys->b[2];
+        p.vbt = ys->bt[2];
+    }
     constexpr int rows_per_wg = (kKvThreads / 64) * (64 / (HD / 4));
     const int n_items = n_tok * ctx->n_kv_heads;
-    hipLaunchKernelGGL(prefill_kv_kernel<HD>, dim3((n_items + rows_per_wg - 1) / rows_per_wg), dim3(kKvThreads),
+    hipLaunchKernelGGL((prefill_kv_kernel<HD, YS>), dim3((n_items + rows_per_wg - 1) / rows_per_wg), dim3(kKvThreads),
                        0, ctx->stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -610,18 +692,39 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     a.nblk = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
     a.rope = ctx->rope_style;
     a.qscale = 1.4426950408889634f / sqrtf((float)HD);
+    a.q_ld = (int)ctx->q_dim;
+    a.qw = a.x_inv = nullptr;
+    a.qb = nullptr;
+    a.qbt = 0;
+    if (YS) {
+        a.q = ys->y;
+        a.q_ld = ys->ld;
+        a.qw = ys->w_inv;
+        a.x_inv = ys->x_inv;
+        a.qb = ys->b[0];
+        a.qbt = ys->bt[0];
+    }
     dim3 grid((a.nblk + 1) / 2 * ctx->n_kv_heads);  // pairs of row blocks
-    if (ctx->prefill_split_q)
-        hipLaunchKernelGGL((prefill_attn_kernel<HD, true>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
+    const bool split_q = ctx->prefill_split_q > 0 || (ctx->prefill_split_q < 0 && !norm);
+    if (split_q)
+        hipLaunchKernelGGL((prefill_attn_kernel<HD, true, YS>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     else
-        hipLaunchKernelGGL((prefill_attn_kernel<HD, false>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
+        hipLaunchKernelGGL((prefill_attn_kernel<HD, false, YS>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
                           const float* k, const float* v, float* out) {
-    if (ctx->head_dim == 64) return launch_prefill_hd<64>(ctx, layer, start, n_tok, q, k, v, out);
-    if (ctx->head_dim == 128) return launch_prefill_hd<128>(ctx, layer, start, n_tok, q, k, v, out);
+    if (ctx->head_dim == 64) return launch_prefill_hd<64, false>(ctx, layer, start, n_tok, q, k, v, out, nullptr);
+    if (ctx->head_dim == 128) return launch_prefill_hd<128, false>(ctx, layer, start, n_tok, q, k, v, out, nullptr);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, const PrefillScaled& ys, float* out) {
+    if (ctx->head_dim == 64)
+        return launch_prefill_hd<64, true>(ctx, layer, start, n_tok, nullptr, nullptr, nullptr, out, &ys);
+    if (ctx->head_dim == 128)
+        return launch_prefill_hd<128, true>(ctx, layer, start, n_tok, nullptr, nullptr, nullptr, out, &ys);
     return hipErrorInvalidValue;
 }
 

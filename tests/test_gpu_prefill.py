@@ -9,6 +9,7 @@ from gpu_util import assert_bits_equal, assert_close
 
 torch = pytest.importorskip("torch")
 from picolm_qwen_amd import PicoAttention  # noqa: E402
+from picolm_qwen_amd._lib import PQA_ERR_ARG, PQAError, check, lib  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +71,17 @@ def test_prefill_to_last_table_row_without_qk_norm():
     # a table that ends on an allocation boundary, no QK-norm.
     print("prefill to last row, no qk-norm", flush=True)
     _prefill_case(41, 16, 8, 128, 65536, 0, 1e6, False, 65536 - 300, 300, 0.0)
+
+
+def test_prefill_precision_setting_values():
+    # -1 (per layer, the default), 0 and 1 are the modes; anything else is refused
+    att = PicoAttention(1, 16, 4, 2, 64)
+    for mode in (None, False, True):
+        att.set_prefill_precision(mode)
+    with pytest.raises(PQAError) as e:
+        check(lib().pqa_set_prefill_precision(att.handle, 2), att.handle)
+    assert e.value.code == PQA_ERR_ARG
+    att.close()
 
 
 def test_prefill_split_q_mode_on_plain_inputs():

@@ -271,6 +271,42 @@ def test_batched_projection_follows_replaced_weights():
     att.close()
 
 
+def test_prompt_path_from_xb_with_biases():
+    # Qwen2.5-style layer: q/k/v biases (F32 and F16), no QK-norm, hd 64,
+    # a prompt continuing at position 40; the prefill kernels read the scaled
+    # GEMM result, undo the scale and add the biases themselves. q and k here
+    # have std 2 (scores up to ~11): a layer without QK-norm takes the split-q
+    # scores by default, and one fp16 q would miss the tolerance
+    print("prefill_x with biases", flush=True)
+    rng = np.random.default_rng(1414)
+    nh, nkv, hd, dim, n_tok, smax, start = 14, 2, 64, 896, 70, 160, 40
+    cos, sin = O.rope_table(1e6, hd, smax)
+    att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    mats = [(make_rows(rng, O.GGUF_Q8_0, nh * hd, dim), make_bias(rng, O.GGUF_F32, nh * hd), O.GGUF_F32),
+            (make_rows(rng, O.GGUF_Q8_0, nkv * hd, dim), make_bias(rng, O.GGUF_F16, nkv * hd), O.GGUF_F16),
+            (make_rows(rng, O.GGUF_Q8_0, nkv * hd, dim), make_bias(rng, O.GGUF_F32, nkv * hd), O.GGUF_F32)]
+    att.set_qkv_weights(0, dim, mats[0][0], O.GGUF_Q8_0, mats[1][0], O.GGUF_Q8_0, mats[2][0], O.GGUF_Q8_0,
+                        mats[0][1], mats[0][2], mats[1][1], mats[1][2], mats[2][1], mats[2][2])
+    kc = np.zeros((smax, nkv * hd), np.uint16)
+    vc = np.zeros((smax, nkv * hd), np.uint16)
+    hk, hv = O.synth_kv_rows(77, 0, nkv * hd, 0, start, 0.0, 4)
+    kc[:start], vc[:start] = hk, hv
+    att.kv_upload(0, 0, hk, hv)
+    x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    qkv = [np.stack([O.matmul_bias(x[t], w, O.GGUF_Q8_0, w.shape[0], b, bt) for t in range(n_tok)])
+           for w, b, bt in mats]
+    want = O.prefill(O.shape(nh, nkv, hd, smax, 0), start, *qkv, None, None, cos, sin, kc, vc)
+    out = att.forward_batch_x(0, start, torch.from_numpy(x).to(torch.device("cuda:0"))).cpu().numpy()
+    assert_close(out, want)
+    gk, gv = att.kv_download(0, start, n_tok)
+    for name, g, wnt in (("K", gk, kc[start:start + n_tok]), ("V", gv, vc[start:start + n_tok])):
+        same = g == wnt
+        gf, wf = g.view(np.float16).astype(np.float64), wnt.view(np.float16).astype(np.float64)
+        slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
+        assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
+    att.close()
+
+
 def test_prompt_path_from_xb_matches_oracle():
     # pqa_prefill_x = batched projections + the MFMA prefill: outputs within the
     # attention tolerance; K rows carry the projection's reordering, so a few
