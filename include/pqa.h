@@ -257,12 +257,11 @@ int pqa_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float 
 int pqa_set_decode_split(pqa_ctx* ctx, int rows_per_split);
 
 /* Prefill score precision.
- * 0: q is rounded once to fp16 for the QK^T MFMA, an error of about 2.5e-4
- *    per score at unit-variance inputs, growing with |q| |k|.
- * 1: q is carried as fp16 hi + lo (two MFMAs per step), fp32-level scores;
- *    costs 1.5x the score MFMA work (about 13 % of a Qwen3-4B prefill).
- * -1 (default): 1 in layers without QK-norm, whose q and k come straight from
- *    the projections and are unbounded; 0 in layers with QK-norm. */
+ * 1 (default): q is carried as fp16 hi + lo (two MFMAs per k-step),
+ *    fp32-level scores.
+ * 0: q is rounded once to fp16 for the QK^T MFMA: about 13 % faster on a
+ *    Qwen3-4B prefill, but the score error grows with |q| |k| (QK-norm
+ *    weights of 2 already put outputs past max-abs 2e-3 / rel 1e-2). */
 int pqa_set_prefill_precision(pqa_ctx* ctx, int split_q);
 
 #ifdef __cplusplus

@@ -139,11 +139,10 @@ class PicoAttention:
     def set_decode_split(self, rows_per_split: int) -> None:
         check(lib().pqa_set_decode_split(self.handle, rows_per_split), self.handle)
 
-    def set_prefill_precision(self, split_q) -> None:
-        """True: prefill scores from q as fp16 hi + lo everywhere; False: one fp16
-        q everywhere; None (the default): hi + lo in layers without QK-norm."""
-        mode = -1 if split_q is None else int(bool(split_q))
-        check(lib().pqa_set_prefill_precision(self.handle, mode), self.handle)
+    def set_prefill_precision(self, split_q: bool) -> None:
+        """True (the default): prefill scores from q as fp16 hi + lo; False: one
+        fp16 q (faster; its score error grows with |q| |k|)."""
+        check(lib().pqa_set_prefill_precision(self.handle, int(bool(split_q))), self.handle)
 
     # -- the block ----------------------------------------------------------
     def set_qk_norm(self, layer: int, q_norm_w, k_norm_w) -> None:

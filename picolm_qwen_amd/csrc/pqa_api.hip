@@ -307,7 +307,7 @@ extern "C" int pqa_set_decode_split(pqa_ctx* ctx, int rows_per_split) {
 
 extern "C" int pqa_set_prefill_precision(pqa_ctx* ctx, int split_q) {
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_prefill_precision: ctx is NULL");
-    if (split_q < -1 || split_q > 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_prefill_precision: -1, 0 or 1");
+    if (split_q != 0 && split_q != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_prefill_precision: 0 or 1");
     ctx->prefill_split_q = split_q;
     return PQA_OK;
 }

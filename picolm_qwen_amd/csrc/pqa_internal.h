@@ -52,9 +52,9 @@ struct pqa_ctx {
     int cu_count = 256;
 
     // prefill: q = fp16 hi + lo in the score products (outlier-heavy caches)
-    // -1 (default): q as fp16 hi + lo in layers without QK-norm (their q and k
-    // are unbounded), one fp16 q in layers with it; 0 / 1: that mode everywhere
-    int prefill_split_q = -1;
+    // prefill q: 1 (default) fp16 hi + lo, fp32-level scores; 0 one fp16 q,
+    // whose score error grows with |q| |k|
+    int prefill_split_q = 1;
 
     // projections (pqa_set_qkv_weights) and the q/k/v of pqa_decode_x
     std::vector<pqa_proj_weights> proj;

@@ -705,8 +705,7 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
         a.qbt = ys->bt[0];
     }
     dim3 grid((a.nblk + 1) / 2 * ctx->n_kv_heads);  // pairs of row blocks
-    const bool split_q = ctx->prefill_split_q > 0 || (ctx->prefill_split_q < 0 && !norm);
-    if (split_q)
+    if (ctx->prefill_split_q)
         hipLaunchKernelGGL((prefill_attn_kernel<HD, true, YS>), grid, dim3(kAttnThreads), 0, ctx->stream, a);
     else
         hipLaunchKernelGGL((prefill_attn_kernel<HD, false, YS>), grid, dim3(kAttnThreads), 0, ctx->stream, a);

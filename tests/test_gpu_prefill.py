@@ -14,8 +14,9 @@ from picolm_qwen_amd._lib import PQA_ERR_ARG, PQAError, check, lib  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 # name, n_heads, n_kv, head_dim, max_seq_len, rope_style, rope_base, qk_norm, start, n_tok, history_outliers
-# Cases whose history has x8 outlier rows run with the split-q precision mode:
-# a single fp16 rounding of q moves those scores by ~1e-2 (see pqa.h).
+# Every case runs in the default precision (q as fp16 hi + lo). The cases
+# without outliers also run with one fp16 q; with x8 outlier rows in the
+# history a single fp16 rounding of q moves those scores by ~1e-2.
 CASES = [
     ("qwen3_4b_s256", 32, 8, 128, 256, 0, 1e6, True, 0, 256, 0.0),
     ("qwen3_4b_start37_n200", 32, 8, 128, 512, 0, 1e6, True, 37, 200, 0.0),
@@ -30,15 +31,20 @@ CASES = [
 ]
 
 
-def _prefill_case(idx, nh, nkv, hd, smax, style, base, qk, start, n_tok, prob, split_q=False):
+def _prefill_case(idx, nh, nkv, hd, smax, style, base, qk, start, n_tok, prob, split_q=None,
+                  norm_scale=1.0):
+    """split_q None keeps the library's default precision; norm_scale
+    multiplies the QK-norm weights (trained ones are not pinned near 1)."""
     seed = 9000 + idx
     kvd = nkv * hd
     cos, sin = O.rope_table(base, hd, smax)
     att = PicoAttention(1, smax, nh, nkv, hd, style, rope_cos=cos, rope_sin=sin)
-    att.set_prefill_precision(prob > 0 or split_q)
+    if split_q is not None:
+        att.set_prefill_precision(split_q)
     qn = kn = None
     if qk:
         qn, kn = O.qk_norm_weights(seed, 0, hd)
+        qn, kn = (qn * norm_scale).astype(np.float32), (kn * norm_scale).astype(np.float32)
         att.set_qk_norm(0, qn, kn)
     kc = np.zeros((smax, kvd), np.uint16)
     vc = np.zeros((smax, kvd), np.uint16)
@@ -66,6 +72,23 @@ def test_prefill_matches_oracle(case):
     _prefill_case(CASES.index(case), *case[1:])
 
 
+FP16_Q_CASES = [c for c in CASES if c[-1] == 0.0]
+
+
+@pytest.mark.parametrize("case", FP16_Q_CASES, ids=[c[0] for c in FP16_Q_CASES])
+def test_prefill_fp16_q_mode_matches_oracle(case):
+    print(f"prefill fp16-q case {case[0]}", flush=True)
+    _prefill_case(CASES.index(case), *case[1:], split_q=False)
+
+
+@pytest.mark.parametrize("scale", [2.0, 3.0])
+def test_prefill_default_with_large_qk_norm_weights(scale):
+    # QK-norm weights scaled by 2-3 scale every score by 4-9: the default hi + lo
+    # q stays inside the tolerance (one fp16 q misses it from a scale of about 2)
+    print(f"prefill qk-norm weights x{scale}", flush=True)
+    _prefill_case(60, 32, 8, 128, 300, 0, 1e6, True, 20, 250, 0.0, norm_scale=scale)
+
+
 def test_prefill_to_last_table_row_without_qk_norm():
     # Same regression as the decode test: the prompt ends on the last row of
     # a table that ends on an allocation boundary, no QK-norm.
@@ -74,9 +97,9 @@ def test_prefill_to_last_table_row_without_qk_norm():
 
 
 def test_prefill_precision_setting_values():
-    # -1 (per layer, the default), 0 and 1 are the modes; anything else is refused
+    # 1 (hi + lo, the default) and 0 (one fp16 q) are the modes; anything else is refused
     att = PicoAttention(1, 16, 4, 2, 64)
-    for mode in (None, False, True):
+    for mode in (False, True):
         att.set_prefill_precision(mode)
     with pytest.raises(PQAError) as e:
         check(lib().pqa_set_prefill_precision(att.handle, 2), att.handle)
@@ -84,8 +107,8 @@ def test_prefill_precision_setting_values():
     att.close()
 
 
-def test_prefill_split_q_mode_on_plain_inputs():
-    print("prefill split-q mode", flush=True)
+def test_prefill_split_q_mode_set_explicitly():
+    print("prefill split-q mode set explicitly", flush=True)
     _prefill_case(40, 32, 8, 128, 300, 0, 1e6, True, 20, 250, 0.0, split_q=True)
 
 

@@ -275,8 +275,8 @@ def test_prompt_path_from_xb_with_biases():
     # Qwen2.5-style layer: q/k/v biases (F32 and F16), no QK-norm, hd 64,
     # a prompt continuing at position 40; the prefill kernels read the scaled
     # GEMM result, undo the scale and add the biases themselves. q and k here
-    # have std 2 (scores up to ~11): a layer without QK-norm takes the split-q
-    # scores by default, and one fp16 q would miss the tolerance
+    # have std 2 (scores up to ~11): the default hi + lo q keeps the scores at
+    # fp32 level (one fp16 q would miss the tolerance here)
     print("prefill_x with biases", flush=True)
     rng = np.random.default_rng(1414)
     nh, nkv, hd, dim, n_tok, smax, start = 14, 2, 64, 896, 70, 160, 40
