@@ -77,3 +77,51 @@ def test_python_wrapper_raises_without_gpu():
     from picolm_qwen_amd import PicoAttention, PQAError
     with pytest.raises(PQAError):
         PicoAttention(1, 64, 8, 2, 64)
+
+
+CALLER = r"""
+#include "pqa.h"
+#include <stdio.h>
+#include <string.h>
+#include <math.h>
+
+int main(void) {
+    pqa_ctx* ctx = NULL;
+    float tab[64 * 48] = {0};
+    /* the reference's forward loop would create one context per model; a bad
+       head_dim is refused before any device call */
+    int rc = pqa_create(&ctx, 1, 64, 8, 2, 96, PQA_ROPE_NEOX_HALF, tab, tab);
+    if (rc != PQA_ERR_UNSUPPORTED || ctx != NULL) return 1;
+    if (!strstr(pqa_last_error(NULL), "head_dim")) return 2;
+    if (pqa_decode(NULL, 0, 0, NULL, NULL, NULL, NULL) != PQA_ERR_ARG) return 3;
+    float c[4 * 32], s[4 * 32];
+    pqa_rope_table(10000.0f, 64, 4, c, s);
+    for (int pos = 0; pos < 4; pos++)
+        for (int i = 0; i < 32; i++) {
+            float theta = (float)pos / powf(10000.0f, (float)(2 * i) / 64.0f);
+            if (c[pos * 32 + i] != cosf(theta) || s[pos * 32 + i] != sinf(theta)) return 4;
+        }
+    printf("caller ok\n");
+    return 0;
+}
+"""
+
+
+@pytest.mark.parametrize("compiler,std,ext", [("g++", "-std=c++17", "cpp"), ("gcc", "-std=c11", "c")])
+def test_header_compiles_and_links_from_c_and_cpp(tmp_path, compiler, std, ext):
+    # The reference's forward loop is C++17; a C caller works too. The header
+    # must compile warning-free in both and every call must resolve in libpqa.so.
+    import shutil
+    import subprocess
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not installed")
+    src = tmp_path / f"caller.{ext}"
+    src.write_text(CALLER)
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(LIB)
+    cmd = [compiler, std, "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{ROOT}/include", str(src), "-o", str(exe),
+           f"-L{libdir}", "-lpqa", f"-Wl,-rpath,{libdir}", "-lm"]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stderr[-2000:])
+    assert "caller ok" in out.stdout
