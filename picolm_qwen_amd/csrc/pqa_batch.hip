@@ -89,6 +89,16 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
 // 2^s that takes it into [2^14, 2^15), dst row = the hi/lo halves of a 2^s in
 // the order [hi | hi | lo] (weights) or [hi | lo | hi] (inputs), and
 // inv_scale[row] = 2^-s.
+__device__ __forceinline__ float split_max(float mx, float* s_max) {
+    mx = group_max<64>(mx);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    return fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+}
+
+// mx in [2^e, 2^(e+1)): s = 14 - e; an all-zero row keeps s = 0
+__device__ __forceinline__ int split_shift(float mx) { return mx > 0.0f ? min(126, max(-126, 14 - ilogbf(mx))) : 0; }
+
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ src, int n, _Float16* __restrict__ dst,
                                                      float* __restrict__ inv_scale, int x_layout) {
     __shared__ float s_max[4];
@@ -97,12 +107,8 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ s
     _Float16* d = dst + (size_t)row * 3 * n;
     float mx = 0.0f;
     for (int i = tid; i < n; i += 256) mx = fmaxf(mx, fabsf(a[i]));
-    mx = group_max<64>(mx);
-    if ((tid & 63) == 0) s_max[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-    // mx in [2^e, 2^(e+1)): s = 14 - e; an all-zero row keeps s = 0
-    const int s = mx > 0.0f ? min(126, max(-126, 14 - ilogbf(mx))) : 0;
+    mx = split_max(mx, s_max);
+    const int s = split_shift(mx);
     const float sc = ldexpf(1.0f, s);
     if (tid == 0) inv_scale[row] = ldexpf(1.0f, -s);
     for (int i = tid; i < n; i += 256) {
@@ -113,6 +119,57 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ s
         d[n + i] = x_layout ? lo : hi;
         d[2 * n + i] = x_layout ? hi : lo;
     }
+}
+
+// The same split for rows of n % 4 == 0, n <= 256 * 4 * kSplitVec floats, 16-byte
+// aligned: the row is read once into registers as float4s and written as
+// half4s (same arithmetic, same bits).
+constexpr int kSplitVec = 8;
+__global__ __launch_bounds__(256) void split3_vec_kernel(const float* __restrict__ src, int n,
+                                                         _Float16* __restrict__ dst, float* __restrict__ inv_scale,
+                                                         int x_layout) {
+    __shared__ float s_max[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int n4 = n >> 2;
+    const float4* a = (const float4*)(src + (size_t)row * n);
+    _Float16* d = dst + (size_t)row * 3 * n;
+    float4 v[kSplitVec];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kSplitVec; j++) {
+        const int i = tid + 256 * j;
+        v[j] = i < n4 ? a[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+    mx = split_max(mx, s_max);
+    const int s = split_shift(mx);
+    const float sc = ldexpf(1.0f, s);
+    if (tid == 0) inv_scale[row] = ldexpf(1.0f, -s);
+#pragma unroll
+    for (int j = 0; j < kSplitVec; j++) {
+        const int i = tid + 256 * j;
+        if (i >= n4) break;
+        const float x[4] = {v[j].x * sc, v[j].y * sc, v[j].z * sc, v[j].w * sc};
+        half4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            hi[e] = (_Float16)x[e];
+            lo[e] = (_Float16)(x[e] - (float)hi[e]);
+        }
+        *(half4*)(d + 4 * i) = hi;
+        *(half4*)(d + n + 4 * i) = x_layout ? lo : hi;
+        *(half4*)(d + 2 * n + 4 * i) = x_layout ? hi : lo;
+    }
+}
+
+// one workgroup per row of src [rows][n] into dst [rows][3n]
+static void launch_split3(const float* src, int rows, int n, _Float16* dst, float* inv_scale, int x_layout,
+                          hipStream_t stream) {
+    const bool vec = n % 4 == 0 && n <= 256 * 4 * kSplitVec && ((uintptr_t)src & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(split3_vec_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, inv_scale, x_layout);
+    else
+        hipLaunchKernelGGL(split3_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, inv_scale, x_layout);
 }
 
 // The three outputs of the batched GEMM and their biases.
@@ -220,8 +277,7 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     for (int i = 0; i < 3; i++) {
         hipError_t e = pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
         if (e == hipSuccess) {
-            hipLaunchKernelGGL(pqa::split3_kernel, dim3(rows[i]), dim3(256), 0, ctx->stream, (const float*)ctx->wf32, n,
-                               w3 + off * 3 * n, w_inv + off, 0);
+            pqa::launch_split3((const float*)ctx->wf32, rows[i], n, w3 + off * 3 * n, w_inv + off, 0, ctx->stream);
             e = hipGetLastError();
         }
         if (int rc = hip_check(ctx, e, fn)) {
@@ -270,7 +326,7 @@ static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, Split
     const _Float16* w3 = (const _Float16*)p.split;
     *w_inv = (const float*)((const char*)p.split + up256(total * 3 * n * 2));
     if (int rc = ensure_split(ctx, n_tok, n, total, sb, fn)) return rc;
-    hipLaunchKernelGGL(pqa::split3_kernel, dim3(n_tok), dim3(256), 0, ctx->stream, xb, n, sb->x3, sb->x_inv, 1);
+    pqa::launch_split3(xb, n_tok, n, sb->x3, sb->x_inv, 1, ctx->stream);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
     // row-major Y[n_tok][total] = X'[n_tok][3n] W'[total][3n]^T, i.e.
     // column-major C (total x n_tok) = W'^T (total x 3n) * X'^T (3n x n_tok)
