@@ -340,3 +340,26 @@ def test_prompt_path_from_xb_matches_oracle():
         slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
         assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
     att.close()
+
+
+def test_batched_projection_unaligned_input_equals_aligned():
+    # X rows that are not 16-byte aligned take the scalar split kernel, aligned
+    # ones the float4 kernel; both do the same arithmetic, so q, k and v must
+    # agree bit for bit (and with the oracle, through the tests above)
+    print("batched projection, unaligned input", flush=True)
+    rng = np.random.default_rng(5151)
+    nh, nkv, hd, dim, n_tok = 4, 2, 64, 512, 7
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    ws = [make_rows(rng, O.GGUF_Q4_K, rows, dim) for rows in (nh * hd, nkv * hd, nkv * hd)]
+    att.set_qkv_weights(0, dim, ws[0], O.GGUF_Q4_K, ws[1], O.GGUF_Q4_K, ws[2], O.GGUF_Q4_K)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(rng.standard_normal((n_tok, dim)).astype(np.float32)).to(dev)
+    flat = torch.empty(n_tok * dim + 1, dtype=torch.float32, device=dev)
+    xu = flat[1:].view(n_tok, dim)
+    xu.copy_(x)
+    assert xu.data_ptr() % 16 == 4
+    a = [g.cpu().numpy() for g in att.qkv_project_batch(0, x)]
+    b = [g.cpu().numpy() for g in att.qkv_project_batch(0, xu)]
+    for name, ga, gb in zip("qkv", a, b):
+        assert_bits_equal(gb, ga, f"{name} from unaligned rows")
+    att.close()
