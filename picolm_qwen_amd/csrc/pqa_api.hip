@@ -35,7 +35,7 @@ static void free_ctx(pqa_ctx* c) {
     pqa_free_projections(c);
     pqa_free_batch(c);
     void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm, c->part_acc,
-                    c->part_ml,   c->stage,     c->tickets,  c->qkv};
+                    c->part_ml,   c->stage,     c->qkv};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int i = 0; i < 2; ++i) {
@@ -110,8 +110,6 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
     chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
     chk(dev_alloc(&c->qkv, 2 * c->q_dim + 2 * c->kv_dim), "workspace");
-    // one counter per decode column group; groups are single columns at most
-    if (chk(dev_alloc(&c->tickets, (size_t)ny), "workspace")) chk(hipMemset(c->tickets, 0, (size_t)ny * 4), "memset");
     if (rc == PQA_OK) chk(hipDeviceSynchronize(), "sync");
     if (rc != PQA_OK) {
         free_ctx(c);

@@ -55,9 +55,7 @@ struct DecodeArgs {
     float* out;
     float* part_acc;  // [ny][nsplit][G][HD]
     float* part_ml;   // [ny][nsplit][G][2]
-    unsigned* tickets;  // [gridDim.y] finished-split counters (zero between launches)
     int pos, g, nchunk, ny, rope, kv_dim, nsplit, rows_per_split;
-    int fused;  // the last workgroup of a column group merges the splits
     int cpw;    // columns per workgroup: 8 (whole cache rows) or 1 (short histories)
     float qscale;
 };
@@ -68,8 +66,6 @@ constexpr int kDecodeTiles = 2;  // 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 32;  // head dims per combine workgroup
 constexpr int kMaxCombineSplits = 256;
-constexpr int kFusedWeights = 2048;  // (column, head, split) weights the in-kernel merge holds in LDS
-constexpr int kFusedSplits = 64;     // splits the in-kernel merge takes (one lane each)
 constexpr int kShortRowsPerWave = 64;  // per-column workgroups: history rows per wave
 
 template <int HD, int G>
@@ -401,98 +397,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             if (d4 == 0) *(float2*)(a.part_ml + pb * 2) = float2{M, L};
         }
     }
-    if (!a.fused) return;
-
-    // ---------------- last workgroup of the column group merges the splits ----------------
-    // Release: every thread's partial stores are written back to memory
-    // before thread 0 takes a ticket; the workgroup holding the last ticket
-    // invalidates its cache (acquire) and reads all splits of its columns.
-    // M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s,
-    // as decode_combine_kernel does.
-    __shared__ unsigned s_ticket;
-    __shared__ float s_cw[kFusedWeights];
-    __shared__ __attribute__((aligned(16))) float s_cl[kFusedWeights];  // the SG partial sums (float4)
-    static_assert(kFusedWeights >= 4 * kDecodeThreads, "one float4 partial per thread");
-    __shared__ float s_cL[NW * G];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0)
-        s_ticket = __hip_atomic_fetch_add(&a.tickets[blockIdx.y], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_ticket != (unsigned)a.nsplit - 1) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const int npair = cols * G;
-    const int ns = a.nsplit;
-    // Thread (item, split group): item = (pair, float4 of dims); the SG
-    // threads of an item take splits sg, sg + SG, ... and add up through LDS;
-    // with more items than threads SG is 1 and the items take several passes.
-    // The first pass's first FU partial loads go out before the (m, l) round
-    // trip, so the two overlap.
-    constexpr int FU = 16;
-    const int items = npair * D4;
-    const int SG = max(1, min(ns, kDecodeThreads / items));
-    const int per_pass = kDecodeThreads / SG;
-    const int sgi = tid % SG;
-    const size_t sstride = (size_t)G * HD / 4;
-    auto item_src = [&](int item) {  // (pair, float4) of an item; out-of-range items read item 0
-        const int it = item < items ? item : 0;
-        const int pr = it / D4, d4 = it - (it / D4) * D4;
-        const int pc = pr / G, ph = pr - pc * G;
-        return (const floatx4*)(a.part_acc + ((size_t)(ybase + pc) * ns * G + ph) * HD) + d4;
-    };
-    floatx4 v[FU];
-    {
-        const floatx4* src = item_src(tid / SG);
-#pragma unroll
-        for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + u * SG, ns - 1) * sstride];
-    }
-    for (int p2 = w; p2 < npair; p2 += NW) {  // one wave per (column, head), one lane per split
-        const int cc = p2 / G, h = p2 - cc * G;
-        const bool ok = lane < ns;
-        const float2 ml = ok ? *(const float2*)(a.part_ml + (((size_t)(ybase + cc) * ns + lane) * G + h) * 2)
-                             : float2{NEG_INF, 0.0f};
-        const float M = group_max<64>(ml.x);
-        const float wt = ok ? fast_exp2(ml.x - M) : 0.0f;
-        const float L = group_sum<64>(wt * ml.y);
-        if (ok) s_cw[p2 * ns + lane] = wt;
-        if (lane == 0) s_cL[p2] = L;
-    }
-    __syncthreads();
-    floatx4* red = (floatx4*)s_cl;  // SG partial sums per item
-    for (int it0 = 0; it0 < items; it0 += per_pass) {
-        const int item = it0 + tid / SG;
-        const bool has = tid < per_pass * SG && item < items;
-        const int pr = has ? item / D4 : 0, d4 = has ? item - (item / D4) * D4 : 0;
-        const int nmine = has ? (ns - sgi + SG - 1) / SG : 0;
-        const floatx4* src = item_src(has ? item : 0);
-        if (it0 > 0) {
-#pragma unroll
-            for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + u * SG, ns - 1) * sstride];
-        }
-        floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int u = 0; u < FU; u++)
-            if (u < nmine) A += s_cw[pr * ns + sgi + u * SG] * v[u];
-        for (int u0 = FU; u0 < nmine; u0 += FU) {  // more splits than one batch
-#pragma unroll
-            for (int u = 0; u < FU; u++) v[u] = src[(size_t)min(sgi + (u0 + u) * SG, ns - 1) * sstride];
-#pragma unroll
-            for (int u = 0; u < FU; u++)
-                if (u0 + u < nmine) A += s_cw[pr * ns + sgi + (u0 + u) * SG] * v[u];
-        }
-        red[tid] = A;
-        __syncthreads();
-        if (has && sgi == 0) {
-            for (int j = 1; j < SG; j++) A += red[tid + j];
-            const int pc = pr / G, ph = pr - pc * G;
-            const int yk = (ybase + pc) / a.nchunk;
-            const int yc = ybase + pc - yk * a.nchunk;
-            if (ph < min(G, a.g - yc * G))
-                ((floatx4*)(a.out + (size_t)(yk * a.g + yc * G + ph) * HD))[d4] = A * (1.0f / s_cL[pr]);
-        }
-        __syncthreads();  // red is reused by the next pass
-    }
-    if (tid == 0) __hip_atomic_store(&a.tickets[blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge of the split partials of one column: workgroup (head h, column y,
@@ -580,7 +484,7 @@ void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit
         // quarter of the CUs.
         const int rps = kDecodeWaves * kShortRowsPerWave;
         const int ns = std::max(1, (hist + rps - 1) / rps);
-        if (ns * ny <= ctx->cu_count / 4 && ns <= kFusedSplits) {
+        if (ns * ny <= ctx->cu_count / 4 && ns <= kMaxCombineSplits) {
             *rows_per_split = rps;
             *nsplit = ns;
             *cols_per_wg = 1;
@@ -622,7 +526,7 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStr
         default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.nsplit == 1 || a.fused) return e;
+    if (e != hipSuccess || a.nsplit == 1) return e;
     if (a.nsplit > kMaxCombineSplits) return hipErrorInvalidValue;
     hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(kCombineThreads), 0, st,
                        a.part_acc,
@@ -657,8 +561,6 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     decode_split(ctx, pos, &a.rows_per_split, &a.nsplit, &a.cpw);
     // Few splits: the last workgroup of each column group merges them in the
     // same launch; many: a separate merge launch spreads the reads.
-    a.fused = a.nsplit > 1 && a.nsplit <= kFusedSplits && a.cpw * ctx->chunk_heads * a.nsplit <= kFusedWeights;
-    a.tickets = ctx->tickets;
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid(a.nsplit, (a.ny + a.cpw - 1) / a.cpw);
     if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, grid, ctx->stream);

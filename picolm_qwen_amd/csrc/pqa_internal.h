@@ -47,7 +47,6 @@ struct pqa_ctx {
     float* part_acc = nullptr;      // [n_kv*n_chunk][max_splits][chunk_heads][head_dim]
     float* part_ml = nullptr;       // [n_kv*n_chunk][max_splits][chunk_heads][2]
     int max_splits = 0;
-    unsigned* tickets = nullptr;    // [columns] finished-split counters of the in-kernel merge
     int split_override = 0;
     int cu_count = 256;
 
