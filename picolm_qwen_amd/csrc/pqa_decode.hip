@@ -66,7 +66,7 @@ constexpr int kDecodeTiles = 2;  // 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 32;  // head dims per combine workgroup
 constexpr int kMaxCombineSplits = 256;
-constexpr int kShortRowsPerWave = 64;  // per-column workgroups: history rows per wave
+constexpr int kShortRowsPerWave = 16;  // per-column workgroups: history rows per wave (one tile)
 
 template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
@@ -478,10 +478,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
 void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit, int* cols_per_wg) {
     const int ny = ctx->n_kv_heads * ctx->n_chunk;
     if (ctx->split_override <= 0) {
-        // Short histories: one workgroup per column, its 8 waves on 64 rows
-        // each, so the history takes few splits (often one) and the chain of
-        // round trips stays short; used while these workgroups fill at most a
-        // quarter of the CUs.
+        // Short histories: one workgroup per column and split, its 8 waves on
+        // one 16-row tile each, so every wave's loads go out in one round trip
+        // and the splits merge in the combine launch; used while these
+        // workgroups fill at most a quarter of the CUs. (64 rows per wave, one
+        // split for C1, measured 14 % slower over the Qwen2.5-0.5B sweep.)
         const int rps = kDecodeWaves * kShortRowsPerWave;
         const int ns = std::max(1, (hist + rps - 1) / rps);
         if (ns * ny <= ctx->cu_count / 4 && ns <= kMaxCombineSplits) {
