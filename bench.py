@@ -177,6 +177,7 @@ def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4
     res = {"workload": "qwen3_4b_prefill", "n_layers": n_layers, "n_tok": s,
            "us_per_layer_append_plus_attention": round(per_layer_us, 3), "flops_per_layer": fl,
            "TFLOP_per_s": round(tf, 1), "mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "dtype": "fp16",
+           "q_precision": "fp16 hi + lo (the library default; the QK^T MFMA work counts once in flops)",
            "ms_per_step_event": round(ev, 4), "ms_per_step_wall": round(wall, 4)}
     log(f"[bench] prefill: {per_layer_us:.2f} us/layer, {tf:.1f} TFLOP/s ({100 * tf / MFMA_FP16_PEAK_TFLOPS:.1f}% MFMA)")
     cx.close()
