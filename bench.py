@@ -544,6 +544,59 @@ def summarize_pmc(fetch_dir, write_dir):
     return "\n".join(lines)
 
 
+def summarize_counters(dirs, match):
+    """Per-dispatch averages of every counter in one or more rocprofv3 --pmc
+    output directories, for the kernels whose name contains `match`, with the
+    derived rates the counters give: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE x 1024 SIMDs), LDS bank conflicts per LDS instruction,
+    VALU and LDS instructions per MFMA."""
+    vals = {}
+    names = set()
+    durs = []
+    for d in dirs:
+        seen = set()
+        for r in _rows(_find(d, "counter_collection.csv")):
+            name = r["Kernel_Name"]
+            if match not in name:
+                continue
+            names.add(name.split("(")[0])
+            key = (d, r["Dispatch_Id"])  # dispatch ids restart in every run
+            per = vals.setdefault(r["Counter_Name"], {})
+            per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+            if key not in seen:
+                seen.add(key)
+                durs.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+    avg = {c: sum(v.values()) / len(v) for c, v in vals.items()}
+    dur = sum(durs) / len(durs) if durs else 0.0
+    lines = [f"kernel: {' | '.join(sorted(names))}",
+             f"average dispatch duration under counter collection: {dur * 1e6:.2f} us",
+             f"{'counter':32s} {'dispatches':>10s} {'average per dispatch':>22s}"]
+    for c in sorted(avg):
+        lines.append(f"{c:32s} {len(vals[c]):10d} {avg[c]:22.1f}")
+    lines.append("")
+    simds, xcds = 256 * 4, 8
+    if "GRBM_GUI_ACTIVE" in avg and dur:
+        # GRBM_GUI_ACTIVE comes summed over the 8 XCDs
+        lines.append(f"clock: {avg['GRBM_GUI_ACTIVE'] / xcds / dur / 1e6:.0f} MHz "
+                     f"(GRBM_GUI_ACTIVE / {xcds} XCDs / duration)")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in avg and "GRBM_GUI_ACTIVE" in avg:
+        lines.append(f"mfma_busy_frac: {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / (avg['GRBM_GUI_ACTIVE'] / xcds * simds):.4f} "
+                     f"(SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs): issued MFMA "
+                     f"cycles, the hi + lo q's second QK product included)")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in avg and "SQ_INSTS_MFMA" in avg and avg["SQ_INSTS_MFMA"]:
+        lines.append(f"cycles_per_mfma: {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / avg['SQ_INSTS_MFMA']:.2f}")
+    if "SQ_LDS_BANK_CONFLICT" in avg and "SQ_LDS_IDX_ACTIVE" in avg and avg["SQ_LDS_IDX_ACTIVE"]:
+        lines.append(f"lds_bank_conflict_frac: {avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_LDS_IDX_ACTIVE']:.4f} "
+                     f"(SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE cycles)")
+    if "SQ_INSTS_MFMA" in avg and avg["SQ_INSTS_MFMA"]:
+        for c in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU"):
+            if c in avg:
+                lines.append(f"{c.lower()}_per_mfma: {avg[c] / avg['SQ_INSTS_MFMA']:.3f}")
+    if "SQ_WAIT_INST_LDS" in avg and "SQ_WAVE_CYCLES" in avg and avg["SQ_WAVE_CYCLES"]:
+        lines.append(f"wait_inst_lds_per_wave_cycle: {avg['SQ_WAIT_INST_LDS'] / avg['SQ_WAVE_CYCLES']:.4f}")
+    return "\n".join(lines)
+
+
 def summarize_trace(trace_dir):
     """Average kernel durations per (kernel, grid) from a rocprofv3
     --kernel-trace CSV, labelled with the workload each instance belongs to."""
@@ -594,7 +647,13 @@ def main():
                     help="run one secondary workload and print it")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_DIR",
+                    help="per-dispatch counter averages of the kernels named by --kernel")
+    ap.add_argument("--kernel", default="prefill_attn_kernel")
     args = ap.parse_args()
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.kernel))
+        return
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc))
         return

@@ -43,14 +43,20 @@ def _is_torch(x) -> bool:
 
 
 def _dev_ptr(t, dtype_name: str, numel: int):
-    if not t.is_cuda:
-        raise ValueError("torch tensors must be on the GPU")
-    if not t.is_contiguous():
-        raise ValueError("tensors must be contiguous")
+    """Device address of a tensor the library reads or writes numel elements
+    of; anything else (another dtype, a strided view, another size, host
+    memory) raises before the call, since a kernel would then access memory
+    outside the tensor."""
+    if not _is_torch(t):
+        raise ValueError(f"expected a torch tensor on the GPU, got {type(t).__name__}")
     if str(t.dtype) != "torch." + dtype_name:
         raise ValueError(f"expected {dtype_name}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("tensors must be contiguous")
     if t.numel() != numel:
         raise ValueError(f"expected {numel} elements, got {t.numel()}")
+    if not t.is_cuda:
+        raise ValueError("torch tensors must be on the GPU")
     return C.c_void_p(t.data_ptr())
 
 
@@ -59,6 +65,53 @@ def _host(x, numel: int):
     if a.size != numel:
         raise ValueError(f"expected {numel} elements, got {a.size}")
     return a
+
+
+def _host_out(out, numel: int):
+    """A host output array the library may write numel floats into."""
+    if out is None:
+        return np.empty(numel, dtype=np.float32)
+    if not (isinstance(out, np.ndarray) and out.dtype == np.float32 and out.flags.c_contiguous
+            and out.flags.writeable and out.size == numel):
+        raise ValueError(f"out must be a writeable C-contiguous float32 array of {numel} elements")
+    return out
+
+
+# GGUF block geometry (elements, bytes per block) of the weight types the
+# projections take, as the reference's dequantize_row_* reads them
+# (cpp/quant.hpp:33-63, :176-281).
+_GGUF_BLOCK = {1: (1, 4), 2: (1, 2), 3: (32, 18), 9: (32, 34), 13: (256, 144), 15: (256, 210)}
+
+
+def _gguf_row_bytes(wtype: int, n: int):
+    """Bytes of one GGUF row of n elements, or None for a type the library
+    rejects itself (PQA_ERR_UNSUPPORTED) or a width that is not whole blocks."""
+    be_bb = _GGUF_BLOCK.get(int(wtype))
+    if be_bb is None or n % be_bb[0]:
+        return None
+    return n // be_bb[0] * be_bb[1]
+
+
+def _host_rows(a, rows: int, wtype: int, n: int, what: str):
+    """A host weight array that holds at least rows GGUF rows of n elements
+    (the library copies rows x row bytes from it)."""
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a)
+    rb = _gguf_row_bytes(wtype, n)
+    if rb is not None and a.nbytes < rows * rb:
+        raise ValueError(f"{what}: {a.nbytes} bytes, need {rows} rows x {rb} bytes")
+    return a
+
+
+def _host_bias(b, rows: int, btype: int, what: str):
+    if b is None or int(btype) == 0:
+        return None
+    b = np.ascontiguousarray(b)
+    need = rows * (4 if int(btype) == 1 else 2)
+    if int(btype) in (1, 2) and b.nbytes < need:
+        raise ValueError(f"{what}: {b.nbytes} bytes, need {need}")
+    return b
 
 
 class PicoAttention:
@@ -74,6 +127,10 @@ class PicoAttention:
         self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
         self.q_dim, self.kv_dim = n_heads * head_dim, n_kv_heads * head_dim
         self.rope_style = rope_style
+        # per layer: the input width of the q/k/v weights and the row count of
+        # attn_output (0 = not set), for the size checks of the device calls
+        self._qkv_embd = [0] * n_layers
+        self._out_rows = [0] * n_layers
         h = C.c_void_p()
         check(lib().pqa_create(C.byref(h), n_layers, max_seq_len, n_heads, n_kv_heads, head_dim, rope_style,
                                rope_cos.ctypes.data_as(C.c_void_p), rope_sin.ctypes.data_as(C.c_void_p)))
@@ -161,14 +218,14 @@ class PicoAttention:
             import torch
             if out is None:
                 out = torch.empty(self.q_dim, dtype=torch.float32, device=q.device)
+            ptrs = (_dev_ptr(q, "float32", self.q_dim), _dev_ptr(k, "float32", self.kv_dim),
+                    _dev_ptr(v, "float32", self.kv_dim), _dev_ptr(out, "float32", self.q_dim))
             ext = self._enter(q.device, (q, k, v, out))
-            check(lib().pqa_decode(self.handle, layer, pos, _dev_ptr(q, "float32", self.q_dim),
-                                   _dev_ptr(k, "float32", self.kv_dim), _dev_ptr(v, "float32", self.kv_dim),
-                                   _dev_ptr(out, "float32", self.q_dim)), self.handle)
+            check(lib().pqa_decode(self.handle, layer, pos, *ptrs), self.handle)
             self._leave(q.device, ext)
             return out
         qh, kh, vh = _host(q, self.q_dim), _host(k, self.kv_dim), _host(v, self.kv_dim)
-        res = np.empty(self.q_dim, dtype=np.float32) if out is None else out
+        res = _host_out(out, self.q_dim)
         check(lib().pqa_decode_host(self.handle, layer, pos, qh.ctypes.data_as(C.c_void_p),
                                     kh.ctypes.data_as(C.c_void_p), vh.ctypes.data_as(C.c_void_p),
                                     res.ctypes.data_as(C.c_void_p)), self.handle)
@@ -182,17 +239,15 @@ class PicoAttention:
             import torch
             if out is None:
                 out = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=q.device)
+            ptrs = (_dev_ptr(q, "float32", n_tok * self.q_dim), _dev_ptr(k, "float32", n_tok * self.kv_dim),
+                    _dev_ptr(v, "float32", n_tok * self.kv_dim), _dev_ptr(out, "float32", n_tok * self.q_dim))
             ext = self._enter(q.device, (q, k, v, out))
-            check(lib().pqa_prefill(self.handle, layer, start_pos, n_tok,
-                                    _dev_ptr(q, "float32", n_tok * self.q_dim),
-                                    _dev_ptr(k, "float32", n_tok * self.kv_dim),
-                                    _dev_ptr(v, "float32", n_tok * self.kv_dim),
-                                    _dev_ptr(out, "float32", n_tok * self.q_dim)), self.handle)
+            check(lib().pqa_prefill(self.handle, layer, start_pos, n_tok, *ptrs), self.handle)
             self._leave(q.device, ext)
             return out
         qh = _host(q, n_tok * self.q_dim)
         kh, vh = _host(k, n_tok * self.kv_dim), _host(v, n_tok * self.kv_dim)
-        res = np.empty((n_tok, self.q_dim), dtype=np.float32) if out is None else out
+        res = _host_out(out, n_tok * self.q_dim).reshape(n_tok, self.q_dim)
         check(lib().pqa_prefill_host(self.handle, layer, start_pos, n_tok, qh.ctypes.data_as(C.c_void_p),
                                      kh.ctypes.data_as(C.c_void_p), vh.ctypes.data_as(C.c_void_p),
                                      res.ctypes.data_as(C.c_void_p)), self.handle)
@@ -225,62 +280,98 @@ class PicoAttention:
     def set_qkv_weights(self, layer: int, n_embd: int, wq, wq_type: int, wk, wk_type: int, wv, wv_type: int,
                         bq=None, bq_type: int = 0, bk=None, bk_type: int = 0, bv=None, bv_type: int = 0) -> None:
         """attn_q/k/v GGUF rows (uint8 arrays, [rows][row bytes]) and optional F32/F16 biases."""
-        keep = []
+        ws = [_host_rows(w, r, t, n_embd, name) for w, r, t, name in
+              ((wq, self.q_dim, wq_type, "wq"), (wk, self.kv_dim, wk_type, "wk"), (wv, self.kv_dim, wv_type, "wv"))]
+        bs = [_host_bias(b, r, t, name) for b, r, t, name in
+              ((bq, self.q_dim, bq_type, "bq"), (bk, self.kv_dim, bk_type, "bk"), (bv, self.kv_dim, bv_type, "bv"))]
 
         def ptr(a):
-            if a is None:
-                return None
-            a = np.ascontiguousarray(a)
-            keep.append(a)
-            return a.ctypes.data_as(C.c_void_p)
-        check(lib().pqa_set_qkv_weights(self.handle, layer, n_embd, ptr(wq), wq_type, ptr(bq), bq_type,
-                                        ptr(wk), wk_type, ptr(bk), bk_type, ptr(wv), wv_type, ptr(bv), bv_type),
-              self.handle)
+            return None if a is None else a.ctypes.data_as(C.c_void_p)
+        self._check_layer(layer)
+        self._qkv_embd[layer] = 0
+        check(lib().pqa_set_qkv_weights(self.handle, layer, n_embd, ptr(ws[0]), wq_type, ptr(bs[0]), bq_type,
+                                        ptr(ws[1]), wk_type, ptr(bs[1]), bk_type, ptr(ws[2]), wv_type, ptr(bs[2]),
+                                        bv_type), self.handle)
+        self._qkv_embd[layer] = int(n_embd)
+
+    def _check_layer(self, layer: int) -> None:
+        if not 0 <= layer < self.n_layers:
+            raise ValueError(f"layer {layer} outside [0, {self.n_layers})")
+
+    def _embd(self, layer: int) -> int:
+        self._check_layer(layer)
+        if not self._qkv_embd[layer]:
+            raise ValueError(f"layer {layer} has no q/k/v weights")
+        return self._qkv_embd[layer]
+
+    def _outr(self, layer: int) -> int:
+        self._check_layer(layer)
+        if not self._out_rows[layer]:
+            raise ValueError(f"layer {layer} has no attn_output weights")
+        return self._out_rows[layer]
+
+    @staticmethod
+    def _tokens(xb, n_embd: int) -> int:
+        """Token count of a [n_tok][n_embd] prompt input."""
+        if xb.dim() != 2 or int(xb.shape[1]) != n_embd:
+            raise ValueError(f"expected xb of shape [n_tok][{n_embd}], got {tuple(xb.shape)}")
+        if int(xb.shape[0]) <= 0:
+            raise ValueError("n_tok must be positive")
+        return int(xb.shape[0])
 
     def qkv_project(self, layer: int, xb, q=None, k=None, v=None):
         """q, k, v = matmul_bias(xb) on the GPU (torch tensors on the device)."""
         import torch
+        n = self._embd(layer)
         dev = xb.device
         q = torch.empty(self.q_dim, dtype=torch.float32, device=dev) if q is None else q
         k = torch.empty(self.kv_dim, dtype=torch.float32, device=dev) if k is None else k
         v = torch.empty(self.kv_dim, dtype=torch.float32, device=dev) if v is None else v
+        ptrs = (_dev_ptr(xb, "float32", n), _dev_ptr(q, "float32", self.q_dim),
+                _dev_ptr(k, "float32", self.kv_dim), _dev_ptr(v, "float32", self.kv_dim))
         ext = self._enter(dev, (xb, q, k, v))
-        check(lib().pqa_qkv_project(self.handle, layer, C.c_void_p(xb.data_ptr()), C.c_void_p(q.data_ptr()),
-                                    C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr())), self.handle)
+        check(lib().pqa_qkv_project(self.handle, layer, *ptrs), self.handle)
         self._leave(dev, ext)
         return q, k, v
 
     def forward_x(self, layer: int, pos: int, xb, out=None):
         """The attention block from the normed input xb: projections, then decode at pos."""
         import torch
+        n = self._embd(layer)
         dev = xb.device
         out = torch.empty(self.q_dim, dtype=torch.float32, device=dev) if out is None else out
+        ptrs = (_dev_ptr(xb, "float32", n), _dev_ptr(out, "float32", self.q_dim))
         ext = self._enter(dev, (xb, out))
-        check(lib().pqa_decode_x(self.handle, layer, pos, C.c_void_p(xb.data_ptr()), C.c_void_p(out.data_ptr())),
-              self.handle)
+        check(lib().pqa_decode_x(self.handle, layer, pos, *ptrs), self.handle)
         self._leave(dev, ext)
         return out
 
     def set_out_weights(self, layer: int, n_embd: int, wo, wo_type: int, bo=None, bo_type: int = 0) -> None:
         """attn_output GGUF rows (uint8 [n_embd][row bytes of q_dim elements]) and an optional bias."""
-        wo = np.ascontiguousarray(wo)
-        b = None if bo is None else np.ascontiguousarray(bo)
-        check(lib().pqa_set_out_weights(self.handle, layer, n_embd, wo.ctypes.data_as(C.c_void_p), wo_type,
-                                        None if b is None else b.ctypes.data_as(C.c_void_p), bo_type), self.handle)
+        wo = _host_rows(wo, n_embd, wo_type, self.q_dim, "wo")
+        b = _host_bias(bo, n_embd, bo_type, "bo")
+        self._check_layer(layer)
+        self._out_rows[layer] = 0
+        check(lib().pqa_set_out_weights(self.handle, layer, n_embd, None if wo is None else wo.ctypes.data_as(C.c_void_p),
+                                        wo_type, None if b is None else b.ctypes.data_as(C.c_void_p), bo_type),
+              self.handle)
+        self._out_rows[layer] = int(n_embd)
 
     def out_project(self, layer: int, attn, x):
         """x += Wo attn + bo (cpp/model.hpp:420-427); torch tensors on the device, x updated in place."""
+        rows = self._outr(layer)
+        ptrs = (_dev_ptr(attn, "float32", self.q_dim), _dev_ptr(x, "float32", rows))
         ext = self._enter(attn.device, (attn, x))
-        check(lib().pqa_out_project(self.handle, layer, C.c_void_p(attn.data_ptr()), C.c_void_p(x.data_ptr())),
-              self.handle)
+        check(lib().pqa_out_project(self.handle, layer, *ptrs), self.handle)
         self._leave(attn.device, ext)
         return x
 
     def attention_block(self, layer: int, pos: int, xb, x):
         """cpp/model.hpp:320-427 from the normed input xb: x += attn_output(attention(q, k, v))."""
+        n, rows = self._embd(layer), self._outr(layer)
+        ptrs = (_dev_ptr(xb, "float32", n), _dev_ptr(x, "float32", rows))
         ext = self._enter(xb.device, (xb, x))
-        check(lib().pqa_attention_block(self.handle, layer, pos, C.c_void_p(xb.data_ptr()), C.c_void_p(x.data_ptr())),
-              self.handle)
+        check(lib().pqa_attention_block(self.handle, layer, pos, *ptrs), self.handle)
         self._leave(xb.device, ext)
         return x
 
@@ -289,26 +380,28 @@ class PicoAttention:
         weights, split into fp16 hi + lo parts with fp32 accumulation (within
         (3 n_embd + 12) 2^-24 sum |w x| of the reference)."""
         import torch
-        n_tok = xb.shape[0]
+        n = self._embd(layer)
+        n_tok = self._tokens(xb, n)
         dev = xb.device
         q = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=dev)
         k = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
         v = torch.empty((n_tok, self.kv_dim), dtype=torch.float32, device=dev)
+        ptrs = (_dev_ptr(xb, "float32", n_tok * n), _dev_ptr(q, "float32", n_tok * self.q_dim),
+                _dev_ptr(k, "float32", n_tok * self.kv_dim), _dev_ptr(v, "float32", n_tok * self.kv_dim))
         ext = self._enter(dev, (xb, q, k, v))
-        check(lib().pqa_qkv_project_batch(self.handle, layer, n_tok, C.c_void_p(xb.data_ptr()),
-                                          C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
-                                          C.c_void_p(v.data_ptr())), self.handle)
+        check(lib().pqa_qkv_project_batch(self.handle, layer, n_tok, *ptrs), self.handle)
         self._leave(dev, ext)
         return q, k, v
 
     def forward_batch_x(self, layer: int, start_pos: int, xb, out=None):
         """The prompt path of a layer from the normed inputs xb [n_tok][n_embd]."""
         import torch
-        n_tok = xb.shape[0]
+        n = self._embd(layer)
+        n_tok = self._tokens(xb, n)
         out = torch.empty((n_tok, self.q_dim), dtype=torch.float32, device=xb.device) if out is None else out
+        ptrs = (_dev_ptr(xb, "float32", n_tok * n), _dev_ptr(out, "float32", n_tok * self.q_dim))
         ext = self._enter(xb.device, (xb, out))
-        check(lib().pqa_prefill_x(self.handle, layer, start_pos, n_tok, C.c_void_p(xb.data_ptr()),
-                                  C.c_void_p(out.data_ptr())), self.handle)
+        check(lib().pqa_prefill_x(self.handle, layer, start_pos, n_tok, *ptrs), self.handle)
         self._leave(xb.device, ext)
         return out
 
@@ -332,7 +425,7 @@ class PicoAttention:
     def fp32_to_fp16(self, src, dst) -> None:
         """Device fp32 -> fp16 with the reference rounding (torch tensors on the GPU)."""
         n = src.numel()
+        ptrs = (_dev_ptr(src, "float32", n), _dev_ptr(dst, "int16", n))
         ext = self._enter(src.device, (src, dst))
-        check(lib().pqa_fp32_to_fp16(self.handle, _dev_ptr(src, "float32", n), _dev_ptr(dst, "int16", n), n),
-              self.handle)
+        check(lib().pqa_fp32_to_fp16(self.handle, *ptrs, n), self.handle)
         self._leave(src.device, ext)

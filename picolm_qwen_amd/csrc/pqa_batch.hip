@@ -353,6 +353,9 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_qkv_project_batch: ctx is NULL");
     if (int rc = check_batch(ctx, layer, n_tok, fn)) return rc;
     if (!xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: NULL buffer");
+    // q/k/v are written as float4s
+    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) != 0)
+        return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: q, k and v must be 16-byte aligned");
     SplitBufs sb;
     const float* w_inv = nullptr;
     if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn)) return rc;

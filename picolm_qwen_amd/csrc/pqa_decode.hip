@@ -566,8 +566,8 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.rope = ctx->rope_style;
     a.kv_dim = (int)ctx->kv_dim;
     decode_split(ctx, pos, &a.rows_per_split, &a.nsplit, &a.cpw);
-    // Few splits: the last workgroup of each column group merges them in the
-    // same launch; many: a separate merge launch spreads the reads.
+    // One split writes the output itself; several write partials that
+    // decode_combine_kernel merges in a second launch.
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid(a.nsplit, (a.ny + a.cpw - 1) / a.cpw);
     if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, grid, ctx->stream);

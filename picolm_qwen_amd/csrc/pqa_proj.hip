@@ -441,10 +441,14 @@ static void free_matrix(pqa_proj_weights& p, int i) {
     p.w[i] = p.b[i] = nullptr;
 }
 
-static int allow_lds(pqa_ctx* ctx, int n, const char* fn) {
-    // x and the chunk rings can exceed the default 64 KB of dynamic LDS
+static int allow_lds(pqa_ctx* ctx, const char* fn) {
+    // x and the chunk rings can exceed the default 64 KB of dynamic LDS. The
+    // attribute belongs to the kernel, process-wide, not to a context or a
+    // layer: it is always set to what the widest allowed input needs, so a
+    // later call for a narrower matrix never lowers it below what another
+    // matrix's launches request.
     return hip_check(ctx, hipFuncSetAttribute((const void*)pqa::proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              (int)pqa::proj_lds_bytes(n)), fn);
+                                              (int)pqa::proj_lds_bytes(PQA_MAX_EMBD)), fn);
 }
 
 extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wq, int wq_type, const void* bq,
@@ -479,7 +483,7 @@ extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
             return rc;
         }
     p.n_embd = n_embd;
-    return allow_lds(ctx, n_embd, fn);
+    return allow_lds(ctx, fn);
 }
 
 extern "C" int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wo, int wo_type, const void* bo,
@@ -504,7 +508,7 @@ extern "C" int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
         return rc;
     }
     p.out_rows = n_embd;
-    return allow_lds(ctx, width, fn);
+    return allow_lds(ctx, fn);
 }
 
 namespace pqa {

@@ -121,9 +121,9 @@ def test_decode_host_and_device_paths_agree():
 
 
 def test_decode_successive_positions():
-    # One context, token after token: the in-kernel split merge hands its
-    # completion counter back to zero for the next call, and each call sees
-    # the rows the previous calls appended.
+    # One context, token after token: each call sees the rows the previous
+    # calls appended, and the split partials of one call (written by the
+    # split pass, read by the combine launch) never leak into the next.
     nh, nkv, hd, smax, pos0, n = 32, 4, 64, 640, 600, 6
     seed = 9100
     cos, sin = O.rope_table(1e4, hd, smax)

@@ -4,6 +4,8 @@ reference's matmul_bias: q, k and v bit-exact for every weight type, with and
 without biases, at small shapes and at the Qwen3-8B layer shape; the attention
 block from xb (pqa_decode_x) with its appended K/V rows bit-exact and its
 output within max-abs 2e-3 / rel 1e-2 of the oracle."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -12,7 +14,7 @@ from gpu_util import assert_bits_equal, assert_close
 from proj_cases import make_bias, make_rows
 
 torch = pytest.importorskip("torch")
-from picolm_qwen_amd import PicoAttention  # noqa: E402
+from picolm_qwen_amd import PicoAttention, _lib  # noqa: E402
 from picolm_qwen_amd._lib import PQA_ERR_ARG, PQA_ERR_UNSUPPORTED, PQAError  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -94,9 +96,45 @@ def test_rejected_shapes_and_types():
         att.set_qkv_weights(0, 256, w, O.GGUF_Q6_K, w, O.GGUF_Q6_K, w, O.GGUF_Q6_K)  # Q6_K needs 512
     assert e.value.code == PQA_ERR_UNSUPPORTED
     dev = torch.device("cuda:0")
-    with pytest.raises(PQAError) as e:
-        att.qkv_project(0, torch.zeros(256, device=dev))
-    assert e.value.code == PQA_ERR_ARG
+    xb = torch.zeros(256, device=dev)
+    with pytest.raises(ValueError):  # the mirror refuses a layer without weights
+        att.qkv_project(0, xb)
+    # and so does the library on its own
+    out = torch.zeros(4 * 64, device=dev)
+    p = [C.c_void_p(t.data_ptr()) for t in (xb, out, out, out)]
+    assert _lib.lib().pqa_qkv_project(att.handle, 0, *p) == PQA_ERR_ARG
+    assert "no projection weights" in att.last_error()
+    att.close()
+
+
+def test_weight_set_order_keeps_the_widest_lds_limit():
+    # Qwen3-4B widths: attn_output rows are 4096 wide (67,584 bytes of LDS per
+    # workgroup, above the default 64 KiB), attn_q/k/v rows 2560 (61,440). The
+    # kernel's LDS limit is process-wide: setting the narrower q/k/v weights
+    # after attn_output must not lower it below what out_project requests.
+    print("out weights, then qkv weights, then out_project", flush=True)
+    rng = np.random.default_rng(4040)
+    nh, nkv, hd, dim = 32, 8, 128, 2560
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    wo = make_rows(rng, O.GGUF_Q4_K, dim, nh * hd)
+    att.set_out_weights(0, dim, wo, O.GGUF_Q4_K)
+    mats = [make_rows(rng, O.GGUF_Q4_K, r, dim) for r in (nh * hd, nkv * hd, nkv * hd)]
+    att.set_qkv_weights(0, dim, mats[0], O.GGUF_Q4_K, mats[1], O.GGUF_Q4_K, mats[2], O.GGUF_Q4_K)
+    dev = torch.device("cuda:0")
+    attn = rng.standard_normal(nh * hd).astype(np.float32)
+    x0 = rng.standard_normal(dim).astype(np.float32)
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.out_project(0, torch.from_numpy(attn).to(dev), x)
+    want = x0 + O.matmul_bias(attn, wo, O.GGUF_Q4_K, dim)
+    assert_bits_equal(x.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32), "x after residual")
+    # a second, narrower context made afterwards does not lower it either
+    small = PicoAttention(1, 16, 4, 2, 64)
+    sm = [make_rows(rng, O.GGUF_Q4_K, r, 512) for r in (256, 128, 128)]
+    small.set_qkv_weights(0, 512, sm[0], O.GGUF_Q4_K, sm[1], O.GGUF_Q4_K, sm[2], O.GGUF_Q4_K)
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.out_project(0, torch.from_numpy(attn).to(dev), x)
+    assert_bits_equal(x.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32), "x, second call")
+    small.close()
     att.close()
 
 
@@ -362,4 +400,24 @@ def test_batched_projection_unaligned_input_equals_aligned():
     b = [g.cpu().numpy() for g in att.qkv_project_batch(0, xu)]
     for name, ga, gb in zip("qkv", a, b):
         assert_bits_equal(gb, ga, f"{name} from unaligned rows")
+    att.close()
+
+
+def test_batched_projection_rejects_unaligned_outputs():
+    # q, k and v are stored as float4s: a misaligned output pointer is refused
+    # (PQA_ERR_ARG) before any kernel runs, as pqa_decode and pqa_prefill do
+    rng = np.random.default_rng(5252)
+    nh, nkv, hd, dim, n_tok = 4, 2, 64, 512, 3
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    ws = [make_rows(rng, O.GGUF_Q4_K, rows, dim) for rows in (nh * hd, nkv * hd, nkv * hd)]
+    att.set_qkv_weights(0, dim, ws[0], O.GGUF_Q4_K, ws[1], O.GGUF_Q4_K, ws[2], O.GGUF_Q4_K)
+    dev = torch.device("cuda:0")
+    x = torch.zeros((n_tok, dim), dtype=torch.float32, device=dev)
+    buf = torch.zeros(n_tok * nh * hd + 8, dtype=torch.float32, device=dev)
+    kv = torch.zeros(n_tok * nkv * hd + 8, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    ptr = lambda t, off=0: C.c_void_p(t.data_ptr() + off)  # noqa: E731
+    for qo, ko, vo in ((4, 0, 0), (0, 8, 0), (0, 0, 12)):
+        rc = L.pqa_qkv_project_batch(att.handle, 0, n_tok, ptr(x), ptr(buf, qo), ptr(kv, ko), ptr(kv, vo))
+        assert rc == PQA_ERR_ARG and "aligned" in att.last_error()
     att.close()
