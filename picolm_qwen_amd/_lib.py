@@ -24,7 +24,7 @@ EXPORTS = [
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
     "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
     "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x", "pqa_set_out_weights", "pqa_out_project",
-    "pqa_attention_block", "pqa_qkv_project_batch", "pqa_prefill_x",
+    "pqa_attention_block", "pqa_qkv_project_batch", "pqa_prefill_x", "pqa_decode_noalloc",
 ]
 
 
@@ -49,6 +49,7 @@ def lib() -> C.CDLL:
     L.pqa_create.argtypes = [C.POINTER(vp), i, i, i, i, i, i, vp, vp]
     L.pqa_set_qk_norm.argtypes = [vp, i, vp, vp]
     L.pqa_decode.argtypes = [vp, i, i, vp, vp, vp, vp]
+    L.pqa_decode_noalloc.argtypes = [vp, i, i, vp, vp, vp, vp]
     L.pqa_prefill.argtypes = [vp, i, i, i, vp, vp, vp, vp]
     L.pqa_decode_host.argtypes = [vp, i, i, vp, vp, vp, vp]
     L.pqa_prefill_host.argtypes = [vp, i, i, i, vp, vp, vp, vp]

@@ -231,6 +231,17 @@ class PicoAttention:
                                     res.ctypes.data_as(C.c_void_p)), self.handle)
         return res
 
+    def forward_noalloc(self, layer: int, pos: int, q, k, v, out):
+        """forward() on device tensors through pqa_decode_noalloc: split
+        partials in the library's static per-GPU scratch, nothing allocated
+        (out must be given). Calls that overlap on one GPU race."""
+        ptrs = (_dev_ptr(q, "float32", self.q_dim), _dev_ptr(k, "float32", self.kv_dim),
+                _dev_ptr(v, "float32", self.kv_dim), _dev_ptr(out, "float32", self.q_dim))
+        ext = self._enter(q.device, (q, k, v, out))
+        check(lib().pqa_decode_noalloc(self.handle, layer, pos, *ptrs), self.handle)
+        self._leave(q.device, ext)
+        return out
+
     def forward_batch(self, layer: int, start_pos: int, q, k, v, out=None):
         """Prompt rows start_pos..start_pos+n-1 (cpp/model.hpp:493-593); q [n][q_dim],
         k/v [n][kv_dim]; returns out [n][q_dim]."""

@@ -110,6 +110,11 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
     chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
     chk(dev_alloc(&c->qkv, 2 * c->q_dim + 2 * c->kv_dim), "workspace");
+    if (rc == PQA_OK) {
+        // the no-allocation decode's scratch address on this device
+        const int src = pqa::scratch_init(c->device);
+        if (src != PQA_OK) rc = src;
+    }
     if (rc == PQA_OK) chk(hipDeviceSynchronize(), "sync");
     if (rc != PQA_OK) {
         free_ctx(c);
@@ -162,7 +167,25 @@ extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, cons
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: NULL buffer");
     if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: buffers must be 16-byte aligned");
-    return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out), "pqa_decode");
+    const pqa::DecodeWorkspace ws{ctx->part_acc, ctx->part_ml, ctx->max_splits};
+    return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out, ws), "pqa_decode");
+}
+
+// pqa_decode with its split partials in the library's static device scratch
+// (pqa_decode.hip) instead of the context's workspace; calls nothing that
+// allocates.
+extern "C" int pqa_decode_noalloc(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
+                                  const float* v, float* out) {
+    static const char* fn = "pqa_decode_noalloc";
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_decode_noalloc: ctx is NULL");
+    if (int rc = check_layer(ctx, layer, fn)) return rc;
+    if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode_noalloc: pos out of range");
+    if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: NULL buffer");
+    if (misaligned(q, k, v, out))
+        return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: buffers must be 16-byte aligned");
+    pqa::DecodeWorkspace ws;
+    if (int rc = pqa::scratch_workspace(ctx, &ws, fn)) return rc;
+    return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out, ws), fn);
 }
 
 extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* q, const float* k,

@@ -35,11 +35,43 @@
 // (log-sum-exp weights); the workgroup writes the output (one split) or its
 // partial (max, sum, acc) per head, and decode_combine_kernel merges splits.
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "pqa_device.h"
 #include "pqa_internal.h"
 
 namespace pqa {
+
+// Split partials of pqa_decode_noalloc: a file-scope device array, so that
+// entry point allocates nothing. Every GPU the library runs on holds its own
+// copy at its own address until the process ends. In host code `scratch` only
+// names the symbol: its device address comes from hipGetSymbolAddress, once
+// per device (scratch_init, called by pqa_create with that device current),
+// and only that address is passed to kernels. Every pqa_decode_noalloc call on
+// one GPU shares the array, so calls that overlap on one GPU (two streams,
+// two threads) race. Nothing in it needs to start at zero: each split writes
+// its whole partial before the combine launch reads it, and the combine reads
+// only the splits of its own call.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kScratchDevices] = {};
+
+int scratch_init(int device) {
+    if (device < 0 || device >= kScratchDevices)
+        return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: device index above 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return PQA_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_err(nullptr, PQA_ERR_HIP,
+                       std::string("pqa_create: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = (float*)p;
+    return PQA_OK;
+}
 
 struct DecodeArgs {
     const float* q;
@@ -481,7 +513,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
     }
 }
 
-void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit, int* cols_per_wg) {
+void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg) {
     const int ny = ctx->n_kv_heads * ctx->n_chunk;
     if (ctx->split_override <= 0) {
         // Short histories: one workgroup per column and split, its 8 waves on
@@ -491,7 +523,7 @@ void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit
         // split for C1, measured 14 % slower over the Qwen2.5-0.5B sweep.)
         const int rps = kDecodeWaves * kShortRowsPerWave;
         const int ns = std::max(1, (hist + rps - 1) / rps);
-        if (ns * ny <= ctx->cu_count / 4 && ns <= kMaxCombineSplits) {
+        if (ns * ny <= ctx->cu_count / 4 && ns <= std::min(kMaxCombineSplits, max_splits)) {
             *rows_per_split = rps;
             *nsplit = ns;
             *cols_per_wg = 1;
@@ -514,13 +546,36 @@ void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit
         rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
     }
     int ns = std::max(1, (hist + rps - 1) / rps);
-    while (ns > ctx->max_splits) {
+    while (ns > max_splits) {
         rps += quantum;
         ns = std::max(1, (hist + rps - 1) / rps);
     }
     *rows_per_split = rps;
     *nsplit = ns;
     *cols_per_wg = cols;
+}
+
+int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
+    float* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (ctx->device >= 0 && ctx->device < kScratchDevices) base = g_scratch_ptr[ctx->device];
+    }
+    if (!base) return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": no scratch address for this device");
+    // As many splits as fit: each takes ny * G * (hd + 2) floats. Fewer splits
+    // than pqa_decode may use only lengthen each split's row range.
+    const size_t ny = (size_t)ctx->n_kv_heads * ctx->n_chunk;
+    const size_t per_split = ny * ctx->chunk_heads * (ctx->head_dim + 2);
+    const size_t fit = kScratchBytes / sizeof(float) / per_split;
+    if (fit < 2)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED,
+                       std::string(fn) + ": the split partials of this head count need " +
+                           std::to_string(2 * per_split * sizeof(float)) + " bytes, above the " +
+                           std::to_string(kScratchBytes) + "-byte scratch");
+    ws->max_splits = (int)std::min<size_t>(fit, (size_t)ctx->max_splits);
+    ws->part_acc = base;
+    ws->part_ml = base + ny * ws->max_splits * ctx->chunk_heads * ctx->head_dim;
+    return PQA_OK;
 }
 
 template <int HD>
@@ -542,7 +597,7 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStr
 }
 
 hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
-                         const float* v, float* out) {
+                         const float* v, float* out, const DecodeWorkspace& ws) {
     DecodeArgs a;
     const int hd = ctx->head_dim;
     a.q = q;
@@ -557,15 +612,15 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.kc = ctx->key_cache + (size_t)layer * ctx->layer_elems;
     a.vc = ctx->val_cache + (size_t)layer * ctx->layer_elems;
     a.out = out;
-    a.part_acc = ctx->part_acc;
-    a.part_ml = ctx->part_ml;
+    a.part_acc = ws.part_acc;
+    a.part_ml = ws.part_ml;
     a.pos = pos;
     a.g = ctx->kv_mul;
     a.nchunk = ctx->n_chunk;
     a.ny = ctx->n_kv_heads * ctx->n_chunk;
     a.rope = ctx->rope_style;
     a.kv_dim = (int)ctx->kv_dim;
-    decode_split(ctx, pos, &a.rows_per_split, &a.nsplit, &a.cpw);
+    decode_split(ctx, pos, ws.max_splits, &a.rows_per_split, &a.nsplit, &a.cpw);
     // One split writes the output itself; several write partials that
     // decode_combine_kernel merges in a second launch.
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);

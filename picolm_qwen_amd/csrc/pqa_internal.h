@@ -87,12 +87,28 @@ namespace pqa {
 int set_err(pqa_ctx* ctx, int code, const std::string& msg);
 int hip_check(pqa_ctx* ctx, hipError_t e, const char* what);
 
-// Rows per decode workgroup, the number of splits and the columns (KV head,
-// chunk) per workgroup for `hist` history rows.
-void decode_split(const pqa_ctx* ctx, int hist, int* rows_per_split, int* nsplit, int* cols_per_wg);
+// Rows per decode workgroup, the number of splits (at most max_splits) and
+// the columns (KV head, chunk) per workgroup for `hist` history rows.
+void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg);
+
+// Where a decode's split partials go: part_acc [ny][splits][G][hd] and
+// part_ml [ny][splits][G][2] floats, for at most max_splits splits.
+struct DecodeWorkspace {
+    float* part_acc;
+    float* part_ml;
+    int max_splits;
+};
 
 hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
-                         const float* v, float* out);
+                         const float* v, float* out, const DecodeWorkspace& ws);
+
+// The no-allocation decode (pqa_decode_noalloc): its split partials live in a
+// file-scope device array of pqa_decode.hip, one per GPU.
+// scratch_init takes that array's address on the current device (once per
+// device, at context creation); scratch_workspace gives the workspace on the
+// context's device, or an error code with ctx->err set.
+int scratch_init(int device);
+int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn);
 hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
                           const float* k, const float* v, float* out);
 // q/k/v of a prompt as the columns of one GEMM result y [n_tok][ld] (q at
