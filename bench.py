@@ -19,9 +19,15 @@ Also reported in the same JSON line under "workloads":
   qwen3_4b_prefill_from_xb  prompt path from the normed inputs: projections + prefill
 
 `roofline` covers the decode kernel of the headline workload, timed with HIP
-events on the library's stream. `cpu_baseline` times the CPU oracle (the
-reference loop restated, heads split over T threads) on one layer of the same
-cache, downloaded from the GPU.
+events on the library's stream. Each attention workload carries a
+`cpu_baseline`: the CPU oracle (the reference's attention loop restated; its
+timing build uses the reference's -O3 and FP contraction with
+-march=x86-64-v4) on the same cache bytes (downloaded) and inputs, on 1
+thread and on T = min(usable cores, 16) threads, with the sample it covers
+stated; the checker build compares the GPU's output and appended rows on the
+layers it lists. `host_entry` times the host-pointer entry points
+(pqa_decode_host, pqa_prefill_host) that a CPU forward loop calls, PCIe and
+the per-call sync included. `cpu_host` names the host CPU.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 """
@@ -93,12 +99,128 @@ def make_inputs(torch, dev, rng, n_layers, n_tok, nh, nkv, hd):
 
 
 def set_norms(cx, rng, hd):
+    """Per-layer QK-RMSNorm weights near 1; returns them as [(q_w, k_w)] by layer."""
+    norms = []
     for layer in range(cx.n_layers):
         qw = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
         kw = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
         cx.check(cx.L.pqa_set_qk_norm(cx.h, layer, qw.ctypes.data_as(C.c_void_p),
                                       kw.ctypes.data_as(C.c_void_p)), cx.h)
-    return
+        norms.append((qw, kw))
+    return norms
+
+
+def _vp(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def cpu_threads():
+    """T = min(usable cores, 16): the reference's thread-pool cap (cpp/tensor.hpp:16)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_host():
+    """This host's core count and CPU model, printed beside every CPU figure."""
+    info = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key = line.split(":", 1)[0].strip()
+                if key in ("model name", "cpu family", "model", "flags") and key not in info:
+                    info[key] = line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+    except OSError:
+        pass
+    flags = set(info.get("flags", "").split())
+    return {"nproc": os.cpu_count(), "usable_cores": len(os.sched_getaffinity(0)),
+            "model": info.get("model name", ""), "family_model": f"{info.get('cpu family')}/{info.get('model')}",
+            "avx512": all(x in flags for x in ("avx512f", "avx512bw", "avx512dq", "avx512vl")),
+            "threads_T": cpu_threads()}
+
+
+def median_time(fn, runs):
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_decode(cx, inputs, norms, style, base, pos, time_layers, check_layers, runs_1, runs_t):
+    """The oracle's decode step (the reference's attention block,
+    cpp/model.hpp:326-418, restated) on this run's own cache bytes and inputs.
+
+    check_layers: the checker build (liboracle.so, heads over T threads) runs
+    each listed layer; its output is compared with the GPU's and its appended
+    K/V row with the row the GPU wrote. time_layers: the timing build
+    (liboracle_bench.so) runs each listed layer on 1 thread (median of
+    runs_1) and on T threads (median of runs_t). inputs(layer) returns the
+    layer's (q, k, v, gpu_out) as host arrays."""
+    import oracle as O
+    from picolm_qwen_amd.attention import rope_table
+    lb, flags = O.bench_lib()
+    nt = cpu_threads()
+    kv_dim = cx.nkv * cx.hd
+    shp = O.shape(cx.nh, cx.nkv, cx.hd, pos + 1, style)
+    cos, sin = rope_table(base, cx.hd, pos + 1)
+    kc = np.empty((pos + 1, kv_dim), np.uint16)
+    vc = np.empty_like(kc)
+    t1, tt, err, exact = [], [], 0.0, True
+    for layer in sorted(set(time_layers) | set(check_layers)):
+        cx.check(cx.L.pqa_kv_download(cx.h, layer, 0, pos + 1, _vp(kc), _vp(vc)), cx.h)
+        krow, vrow = kc[pos].copy(), vc[pos].copy()  # the row the GPU appended
+        q, k, v, got = inputs(layer)
+        qn, kn = norms[layer] if norms else (None, None)
+        if layer in check_layers:
+            want = O.attn_step(shp, pos, q, k, v, qn, kn, cos[pos], sin[pos], kc, vc, nt)
+            err = max(err, float(np.abs(got - want).max()))
+            exact = exact and bool(np.array_equal(kc[pos], krow) and np.array_equal(vc[pos], vrow))
+        if layer in time_layers:
+            def step(n):
+                O.attn_step(shp, pos, q, k, v, qn, kn, cos[pos], sin[pos], kc, vc, n, L=lb)
+            t1.append(median_time(lambda: step(1), runs_1))
+            tt.append(median_time(lambda: step(nt), runs_t))
+    nbytes = decode_bytes(pos + 1, cx.nh, cx.nkv, cx.hd)
+    us1, ust = float(np.mean(t1)) * 1e6, float(np.mean(tt)) * 1e6
+    res = {"value": round(nbytes / ust / 1e3, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+           "us_per_layer": round(ust, 2), "us_per_layer_1_thread": round(us1, 2),
+           "GB_per_s_1_thread": round(nbytes / us1 / 1e3, 3), "build": flags,
+           "layers_timed": len(t1), "runs_per_layer": [runs_1, runs_t],
+           "layers_checked": sorted(check_layers), "gpu_vs_oracle_max_abs_err": err,
+           "appended_kv_rows_bit_exact": exact,
+           "sample": f"the oracle's decode step at pos {pos} on {len(t1)} of {cx.n_layers} layers (same cache "
+                     f"bytes, downloaded, and the same inputs as the GPU run); median of {runs_1} run(s) on 1 "
+                     f"thread and {runs_t} on {nt} threads (query heads split) per layer, mean over layers"}
+    log(f"[bench]   cpu oracle: 1 thread {us1:.1f} us/layer, {nt} threads {ust:.1f} us/layer; "
+        f"layers {sorted(check_layers)} max abs err {err:.2e}, appended rows bit-exact {exact}")
+    return res
+
+
+def host_entry_decode(cx, q, k, v, out, pos, steps):
+    """pqa_decode_host, the call a CPU forward loop makes per layer: host
+    q/k/v in, host out back, PCIe copies and the per-call stream sync
+    included. Returns wall µs per layer and whether its outputs equal the
+    device-pointer entry's bit for bit."""
+    qh, kh, vh, want = (np.ascontiguousarray(t.cpu().numpy()) for t in (q, k, v, out))
+    oh = np.zeros_like(want)
+    fn = cx.L.pqa_decode_host
+    h = cx.h
+    args = [(layer, _vp(qh[layer]), _vp(kh[layer]), _vp(vh[layer]), _vp(oh[layer])) for layer in range(cx.n_layers)]
+
+    def step():
+        for layer, a, b, c, d in args:
+            rc = fn(h, layer, pos, a, b, c, d)
+            if rc:
+                cx.check(rc, h)
+
+    step()
+    t = median_time(step, max(3, steps // 3))
+    return {"entry": "pqa_decode_host", "us_per_layer": round(t * 1e6 / cx.n_layers, 2),
+            "equals_device_entry": bool(np.array_equal(oh, want)),
+            "note": "the caller's pageable host buffers; the payload goes through the library's pinned staging "
+                    "buffer: one H2D copy, the decode, one D2H copy and a stream sync per call"}
 
 
 def timed(torch, cx, fn, steps, warmup):
@@ -122,12 +244,13 @@ def timed(torch, cx, fn, steps, warmup):
 
 
 def decode_workload(torch, dev, name, n_layers, nh, nkv, hd, style, base, pos, prob, steps, warmup, qk_norm,
-                    seed=20251201, keep=False):
+                    seed=20251201, keep=False, cpu=None, host_entry=False):
+    """cpu: None, or (time_layers, check_layers, runs_1, runs_t) for cpu_decode."""
     cx = Ctx(n_layers, pos + 1, nh, nkv, hd, style, base)
     rng = np.random.default_rng(seed)
-    if qk_norm:
-        set_norms(cx, rng, hd)
+    norms = set_norms(cx, rng, hd) if qk_norm else None
     for layer in range(n_layers):
+        # the history stream is keyed by (seed, layer): every layer holds its own rows
         cx.check(cx.L.pqa_synth_kv(cx.h, layer, 0, pos, seed, prob), cx.h)
     q, k, v, out = make_inputs(torch, dev, rng, n_layers, 1, nh, nkv, hd)
     cx.check(cx.L.pqa_sync(cx.h), cx.h)
@@ -149,16 +272,98 @@ def decode_workload(torch, dev, name, n_layers, nh, nkv, hd, style, base, pos, p
            "bytes_per_layer": nbytes, "GB_per_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
            "ms_per_step_event": round(ev, 4), "ms_per_step_wall": round(wall, 4)}
     log(f"[bench] {name}: {per_layer_us:.2f} us/layer, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+    if host_entry:
+        res["host_entry"] = host_entry_decode(cx, q, k, v, out, pos, steps)
+        log(f"[bench]   host entry: {res['host_entry']}")
+    if cpu is not None:
+        def inputs(layer):
+            return tuple(t[layer, 0].cpu().numpy() for t in (q, k, v, out))
+        res["cpu_baseline"] = cpu_decode(cx, inputs, norms, style, base, pos, *cpu)
     if keep:
         return res, cx, (q, k, v, out)
     cx.close()
     return res, None, None
 
 
-def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4242):
+def cpu_prefill(cx, q, k, v, out, norms, s, check_layers, check_rows=512, rows_1=64, rows_t=512):
+    """The oracle's causal prefill (cpp/model.hpp:507-593 restated) on this
+    run's inputs, over the last rows of the prompt with the GPU-built cache
+    of the rows before them (downloaded). The checker build compares the last
+    check_rows rows of each check layer (output at tolerance, appended K/V
+    rows bit for bit); the timing build runs the last rows_1 rows on 1 thread
+    and the last rows_t rows on T threads of layer 0. A row's work is its key
+    count, so the full-layer time is the sample time x (keys of all s rows) /
+    (keys of the sampled rows)."""
+    import oracle as O
+    from picolm_qwen_amd.attention import rope_table
+    lb, flags = O.bench_lib()
+    nt = cpu_threads()
+    kv_dim = cx.nkv * cx.hd
+    shp = O.shape(cx.nh, cx.nkv, cx.hd, s, 0)
+    cos, sin = rope_table(1e6, cx.hd, s)
+    kc = np.empty((s, kv_dim), np.uint16)
+    vc = np.empty_like(kc)
+    keys = lambda r: sum(i + 1 for i in range(s - r, s))  # noqa: E731
+    total = keys(s)
+    err, exact, times = 0.0, True, {}
+    for layer in sorted(set(check_layers) | {0}):
+        cx.check(cx.L.pqa_kv_download(cx.h, layer, 0, s, _vp(kc), _vp(vc)), cx.h)
+        kg, vg = kc.copy(), vc.copy()
+        qh, kh, vh = (t[layer].cpu().numpy() for t in (q, k, v))
+        qn, kn = norms[layer]
+        if layer in check_layers:
+            st = s - check_rows
+            want = O.prefill(shp, st, qh[st:], kh[st:], vh[st:], qn, kn, cos, sin, kc, vc, n_threads=nt)
+            err = max(err, float(np.abs(out[layer, st:].cpu().numpy() - want).max()))
+            exact = exact and bool(np.array_equal(kc, kg) and np.array_equal(vc, vg))
+        if layer == 0:
+            for n, rows in ((1, rows_1), (nt, rows_t)):
+                st = s - rows
+                t0 = time.perf_counter()
+                O.prefill(shp, st, qh[st:], kh[st:], vh[st:], qn, kn, cos, sin, kc, vc, n_threads=n, L=lb)
+                times[n] = (time.perf_counter() - t0) * total / keys(rows)
+    fl = prefill_flops(cx.nh, cx.hd, s)
+    res = {"value": round(fl / times[nt] / 1e12, 5), "unit": "TFLOP/s", "cores": nt, "kind": "port",
+           "us_per_layer": round(times[nt] * 1e6), "us_per_layer_1_thread": round(times[1] * 1e6),
+           "build": flags, "layers_checked": sorted(check_layers), "rows_checked_per_layer": check_rows,
+           "gpu_vs_oracle_max_abs_err": err, "appended_kv_rows_bit_exact": exact,
+           "sample": f"layer 0: the last {rows_1} prompt rows on 1 thread and the last {rows_t} on {nt} threads "
+                     f"(rows split), each run once over the GPU-built cache of the rows before them; "
+                     f"scaled to all {s} rows by key count ({keys(rows_1)} and {keys(rows_t)} of {total} "
+                     f"row-keys). Per layer; the {cx.n_layers}-layer prompt is {cx.n_layers}x."}
+    log(f"[bench]   cpu oracle prefill: 1 thread {times[1]:.2f} s/layer, {nt} threads {times[nt]:.2f} s/layer "
+        f"(extrapolated); layers {sorted(check_layers)} last {check_rows} rows max abs err {err:.2e}, "
+        f"appended rows bit-exact {exact}")
+    return res
+
+
+def host_entry_prefill(cx, q, k, v, out, s):
+    """pqa_prefill_host over all layers: host q/k/v in, host out back, PCIe
+    copies and the per-call sync included; wall µs per layer and whether the
+    outputs equal the device-pointer entry's bit for bit."""
+    qh, kh, vh, want = (np.ascontiguousarray(t.cpu().numpy()) for t in (q, k, v, out))
+    oh = np.zeros_like(want)
+    fn = cx.L.pqa_prefill_host
+    h = cx.h
+
+    def step():
+        for layer in range(cx.n_layers):
+            rc = fn(h, layer, 0, s, _vp(qh[layer]), _vp(kh[layer]), _vp(vh[layer]), _vp(oh[layer]))
+            if rc:
+                cx.check(rc, h)
+
+    step()
+    t = median_time(step, 3)
+    return {"entry": "pqa_prefill_host", "us_per_layer": round(t * 1e6 / cx.n_layers, 1),
+            "equals_device_entry": bool(np.array_equal(oh, want)),
+            "note": "the caller's pageable host buffers (80 MB per layer, past the 4 MiB pinned staging buffer): "
+                    "three H2D copies straight from them, the prefill, one D2H copy and a stream sync per call"}
+
+
+def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4242, cpu=False, host_entry=False):
     cx = Ctx(n_layers, s, nh, nkv, hd, 0, 1e6)
     rng = np.random.default_rng(seed)
-    set_norms(cx, rng, hd)
+    norms = set_norms(cx, rng, hd)
     q, k, v, out = make_inputs(torch, dev, rng, n_layers, s, nh, nkv, hd)
     torch.cuda.synchronize()
     ptr = lambda t, layer: C.c_void_p(t[layer].data_ptr())  # noqa: E731
@@ -180,11 +385,17 @@ def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4
            "q_precision": "fp16 hi + lo (the library default; the QK^T MFMA work counts once in flops)",
            "ms_per_step_event": round(ev, 4), "ms_per_step_wall": round(wall, 4)}
     log(f"[bench] prefill: {per_layer_us:.2f} us/layer, {tf:.1f} TFLOP/s ({100 * tf / MFMA_FP16_PEAK_TFLOPS:.1f}% MFMA)")
+    if host_entry:
+        res["host_entry"] = host_entry_prefill(cx, q, k, v, out, s)
+        log(f"[bench]   host entry: {res['host_entry']}")
+    if cpu:
+        res["cpu_baseline"] = cpu_prefill(cx, q, k, v, out, norms, s, (0, n_layers - 1))
     cx.close()
     return res
 
 
-def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096, checkpoints=(1, 512, 1024, 2048, 4096)):
+def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096, checkpoints=(1, 512, 1024, 2048, 4096),
+                   cpu=False):
     cx = Ctx(n_layers, positions, nh, nkv, hd, 0, 1e6)
     rng = np.random.default_rng(777)
     q, k, v, out = make_inputs(torch, dev, rng, n_layers, positions, nh, nkv, hd)
@@ -216,10 +427,21 @@ def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096,
 
         _, ev = timed(torch, cx, step, 20, 2)
         curve[str(ctx_len)] = round(ev * 1e3 / n_layers, 3)
-    cx.close()
     log(f"[bench] qwen2.5 sweep: avg {avg_us:.2f} us/layer over ctx 1..{positions}; curve {curve}")
-    return {"workload": "qwen2.5_0.5b_sweep", "n_layers": n_layers, "positions": positions,
-            "avg_us_per_layer_launch_loop": round(avg_us, 3), "us_per_layer_vs_ctx": curve}
+    res = {"workload": "qwen2.5_0.5b_sweep", "n_layers": n_layers, "positions": positions,
+           "avg_us_per_layer_launch_loop": round(avg_us, 3), "us_per_layer_vs_ctx": curve}
+    if cpu:
+        # the oracle at two points of the curve, all layers, each layer's own inputs at that position
+        res["cpu_baseline"] = {}
+        for ctx_len in (512, positions):
+            pos = ctx_len - 1
+
+            def inputs(layer, pos=pos):
+                return tuple(t[layer, pos].cpu().numpy() for t in (q, k, v, out))
+            res["cpu_baseline"][str(ctx_len)] = cpu_decode(cx, inputs, None, 0, 1e6, pos, range(n_layers),
+                                                           range(n_layers), 5, 5)
+    cx.close()
+    return res
 
 
 def kvc_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n_pos=4096, reps=3):
@@ -431,49 +653,6 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
     return res
 
 
-def cpu_baseline(cx, q, k, v, out0, nh, nkv, hd, pos, budget_s=12.0):
-    """The oracle (reference attention loop, restated in C) on layer 0 of the
-    headline cache: same K/V bytes (downloaded), same q/k/v and norm weights."""
-    import oracle as O
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    kv_dim = nkv * hd
-    smax = pos + 1
-    kc = np.zeros((smax, kv_dim), np.uint16)
-    vc = np.zeros((smax, kv_dim), np.uint16)
-    cx.check(cx.L.pqa_kv_download(cx.h, 0, 0, pos, kc.ctypes.data_as(C.c_void_p), vc.ctypes.data_as(C.c_void_p)), cx.h)
-    qn = np.empty(hd, np.float32)
-    kn = np.empty(hd, np.float32)
-    rng = np.random.default_rng(20251201)  # same draw order as decode_workload
-    for _ in range(1):
-        qn[:] = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
-        kn[:] = (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
-    from picolm_qwen_amd.attention import rope_table
-    cos, sin = rope_table(1e6, hd, smax)
-    shp = O.shape(nh, nkv, hd, smax, 0)
-    qh, kh, vh = (t[0, 0].cpu().numpy() for t in (q, k, v))
-    t0 = time.perf_counter()
-    want = O.attn_step(shp, pos, qh, kh, vh, qn, kn, cos[pos], sin[pos], kc, vc, 1)
-    t1 = time.perf_counter() - t0
-    got = out0.cpu().numpy().reshape(-1)
-    max_err = float(np.abs(got - want).max())
-    log(f"[bench] layer-0 GPU output vs oracle: max abs err {max_err:.2e}")
-    reps, total = 0, 0.0
-    while total < budget_s and reps < 200:
-        t0 = time.perf_counter()
-        O.attn_step(shp, pos, qh, kh, vh, qn, kn, cos[pos], sin[pos], kc, vc, threads)
-        total += time.perf_counter() - t0
-        reps += 1
-    per_layer = total / reps
-    nbytes = decode_bytes(pos + 1, nh, nkv, hd)
-    log(f"[bench] cpu oracle: 1 thread {t1 * 1e6:.0f} us/layer, {threads} threads {per_layer * 1e6:.0f} us/layer")
-    return {"value": round(nbytes / per_layer / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_layer": round(per_layer * 1e6, 1), "us_per_layer_1_thread": round(t1 * 1e6, 1),
-            "gpu_vs_oracle_max_abs_err": max_err,
-            "sample": f"layer 0 of 36 of the headline decode (pos {pos}, same cache bytes and inputs), "
-                      f"oracle attention step run {reps}x with query heads split over {threads} threads, "
-                      f"plus once on 1 thread"}
-
-
 COPY_BYTES = 1 << 30  # the calibration copy: reads and writes 1 GiB
 
 
@@ -633,6 +812,25 @@ def profile_value(fname, key):
     return None
 
 
+def secondary_workloads(torch, dev, steps, warmup, cpu_on):
+    """The workloads reported beside the headline, in run order (name -> thunk)."""
+    return {
+        # C3: every layer timed on 1 thread once and T threads 3x, every layer checked
+        "qwen3_1.7b_decode": lambda: decode_workload(
+            torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6, 32767, 0.0, steps, warmup, True,
+            cpu=(range(28), range(28), 1, 3) if cpu_on else None, host_entry=True)[0],
+        "qwen3_4b_prefill": lambda: prefill_workload(torch, dev, 36, 32, 8, 128, 2048, max(3, steps // 5), 1,
+                                                     cpu=cpu_on, host_entry=True),
+        "tinyllama_decode": lambda: decode_workload(
+            torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511, 0.0, max(steps, 200), warmup, False,
+            cpu=((0,), (0,), 21, 21) if cpu_on else None, host_entry=True)[0],
+        "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev, cpu=cpu_on),
+        "qwen3_8b_kvc_save_load": lambda: kvc_workload(torch, dev),
+        "qwen3_8b_qkv_proj": lambda: proj_workload(torch, dev, steps=steps, warmup=warmup, cpu=cpu_on),
+        "qwen3_4b_prefill_from_xb": lambda: prefill_x_workload(torch, dev, cpu=cpu_on),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -662,7 +860,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode would shard by KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(decode would shard by KV head with no exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -672,45 +870,26 @@ def main():
     if args.pmc_probe:
         pmc_probe(torch, dev)
         return
+    cpu_on = not args.no_cpu
+    runs = secondary_workloads(torch, dev, args.steps, args.warmup, cpu_on)
     if args.only:
-        runs = {
-            "qwen3_1.7b_decode": lambda: decode_workload(torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6,
-                                                         32767, 0.0, args.steps, args.warmup, True)[0],
-            "qwen3_4b_prefill": lambda: prefill_workload(torch, dev, 36, 32, 8, 128, 2048,
-                                                         max(3, args.steps // 5), 1),
-            "tinyllama_decode": lambda: decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
-                                                        0.0, max(args.steps, 200), args.warmup, False)[0],
-            "qwen2.5_0.5b_sweep": lambda: sweep_workload(torch, dev),
-            "qwen3_8b_kvc_save_load": lambda: kvc_workload(torch, dev),
-            "qwen3_8b_qkv_proj": lambda: proj_workload(torch, dev, steps=args.steps, warmup=args.warmup),
-            "qwen3_4b_prefill_from_xb": lambda: prefill_x_workload(torch, dev),
-        }
         print(json.dumps({args.only: runs[args.only]()}), flush=True)
         return
 
     nh, nkv, hd, layers, pos = 32, 8, 128, 36, 131071
-    head, cx, bufs = decode_workload(torch, dev, "qwen3_8b_decode", layers, nh, nkv, hd, 0, 1e6, pos, 0.01,
-                                     args.steps, args.warmup, True, keep=True)
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(cx, bufs[0], bufs[1], bufs[2], bufs[3][0, 0], nh, nkv, hd, pos)
-    cx.close()
-    del bufs
+    host = cpu_host()
+    log(f"[bench] host CPU: {host}")
+    # C5: 1 thread on layer 0 once, T threads 3x; layers 0, 17 and 35 checked (35's slice starts past 4 GiB)
+    head = decode_workload(torch, dev, "qwen3_8b_decode", layers, nh, nkv, hd, 0, 1e6, pos, 0.01,
+                           args.steps, args.warmup, True, cpu=((0,), (0, 17, 35), 1, 3) if cpu_on else None,
+                           host_entry=not args.quick)[0]
+    cpu = head.get("cpu_baseline")
     torch.cuda.empty_cache()
 
     workloads = {"qwen3_8b_decode": head}
     if not args.quick:
-        workloads["qwen3_1.7b_decode"] = decode_workload(torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6,
-                                                         32767, 0.0, args.steps, args.warmup, True)[0]
-        workloads["qwen3_4b_prefill"] = prefill_workload(torch, dev, 36, 32, 8, 128, 2048,
-                                                         max(3, args.steps // 5), 1)
-        workloads["tinyllama_decode"] = decode_workload(torch, dev, "tinyllama_decode", 1, 32, 4, 64, 1, 1e4, 511,
-                                                        0.0, max(args.steps, 200), args.warmup, False)[0]
-        workloads["qwen2.5_0.5b_sweep"] = sweep_workload(torch, dev)
-        workloads["qwen3_8b_kvc_save_load"] = kvc_workload(torch, dev)
-        workloads["qwen3_8b_qkv_proj"] = proj_workload(torch, dev, steps=args.steps, warmup=args.warmup,
-                                                       cpu=not args.no_cpu)
-        workloads["qwen3_4b_prefill_from_xb"] = prefill_x_workload(torch, dev, cpu=not args.no_cpu)
+        for name, run in runs.items():
+            workloads[name] = run()
 
     per_layer_us = head["us_per_layer"]
     achieved = head["GB_per_s"]
@@ -749,6 +928,7 @@ def main():
                      "traffic_source": "profiles/decode_qwen3_8b_ctx131072_hbm_traffic.txt (rocprofv3 --pmc "
                                        "FETCH_SIZE, WRITE_SIZE; copy-calibrated)"},
         "cpu_baseline": cpu,
+        "cpu_host": host,
         "workloads": workloads,
     }
     print(json.dumps(line), flush=True)

@@ -18,6 +18,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
+ORACLE_BENCH_SO = os.path.join(HERE, "liboracle_bench.so")
 REF_SO = {"A": os.path.join(HERE, "_ref", "libref_A.so"), "B": os.path.join(HERE, "_ref", "libref_B.so"),
           "kvc": os.path.join(HERE, "_ref", "libref_kvc.so")}
 
@@ -35,16 +36,47 @@ class Shape(C.Structure):
 
 
 _lib = None
+_bench_lib = None
+_AVX512 = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
 
 
 def lib():
-    """Loads liboracle.so (built by `make -C oracle`)."""
+    """Loads liboracle.so (built by `make -C oracle`): the checker."""
     global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(ORACLE_SO):
-        raise RuntimeError(f"oracle not built: {ORACLE_SO} missing (run make -C oracle)")
-    L = C.CDLL(ORACLE_SO)
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"oracle not built: {ORACLE_SO} missing (run make -C oracle)")
+        _lib = _bind(C.CDLL(ORACLE_SO))
+    return _lib
+
+
+def host_has_avx512():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return all(x in flags for x in _AVX512)
+    except OSError:
+        pass
+    return False
+
+
+def bench_lib():
+    """The oracle as the reference builds its own code (-O3, FP contraction,
+    x86-64-v4), used only to time the CPU baseline. Returns (library, flags
+    description); falls back to the checker build when liboracle_bench.so is
+    missing or this CPU lacks AVX-512."""
+    global _bench_lib
+    if _bench_lib is None:
+        if os.path.exists(ORACLE_BENCH_SO) and host_has_avx512():
+            _bench_lib = (_bind(C.CDLL(ORACLE_BENCH_SO)), "gcc -O3 -march=x86-64-v4 -ffp-contract=fast")
+        else:
+            _bench_lib = (lib(), "gcc -O3 -march=x86-64-v3 -ffp-contract=off (checker build; no AVX-512 build here)")
+    return _bench_lib
+
+
+def _bind(L):
     L.pqo_fp16_to_fp32.restype = C.c_float
     L.pqo_fp16_to_fp32.argtypes = [C.c_uint16]
     L.pqo_fp32_to_fp16.restype = C.c_uint16
@@ -82,7 +114,6 @@ def lib():
     L.pqo_vec_dot.restype = C.c_float
     L.pqo_vec_dot.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_int]
     L.pqo_matmul_bias.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]
-    _lib = L
     return L
 
 
@@ -148,12 +179,13 @@ def rope_rows(base, head_dim, pos0, n):
     return c, s
 
 
-def attn_step(shp, pos, q, k, v, q_norm_w, k_norm_w, cos_row, sin_row, kc, vc, n_threads=1):
-    """Decode block at `pos`; kc/vc (layer slice, uint16 [S_max, kv_dim]) are updated in place."""
+def attn_step(shp, pos, q, k, v, q_norm_w, k_norm_w, cos_row, sin_row, kc, vc, n_threads=1, L=None):
+    """Decode block at `pos`; kc/vc (layer slice, uint16 [S_max, kv_dim]) are updated in place.
+    L: the library to run (default the checker; bench_lib()[0] for timing)."""
     out = np.empty(shp.n_heads * shp.head_dim, dtype=np.float32)
     qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, dtype=np.float32)
     kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, dtype=np.float32)
-    lib().pqo_attn_step(C.byref(shp), pos, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+    (L or lib()).pqo_attn_step(C.byref(shp), pos, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
                         np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
                         np.ascontiguousarray(v, dtype=np.float32).reshape(-1), _ptr(qn), _ptr(kn),
                         np.ascontiguousarray(cos_row, dtype=np.float32).reshape(-1),
@@ -183,12 +215,12 @@ def append(shp, pos, q, k, v, q_norm_w, k_norm_w, cos_row, sin_row, kc, vc):
 
 
 def prefill(shp, start, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, kc, vc, serial=False,
-            n_threads=8):
+            n_threads=8, L=None):
     n_tok = q.shape[0]
     out = np.empty((n_tok, shp.n_heads * shp.head_dim), dtype=np.float32)
     qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, dtype=np.float32)
     kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, dtype=np.float32)
-    lib().pqo_prefill(C.byref(shp), start, n_tok, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+    (L or lib()).pqo_prefill(C.byref(shp), start, n_tok, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
                       np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
                       np.ascontiguousarray(v, dtype=np.float32).reshape(-1), _ptr(qn), _ptr(kn),
                       np.ascontiguousarray(cos_tab, dtype=np.float32).reshape(-1),

@@ -48,10 +48,11 @@ def build(verbose: bool = False) -> str:
 
 
 def build_oracle(with_reference: bool = True) -> None:
-    """Builds the CPU oracle (test infrastructure) and, when the reference tree
-    is present, the reference harness into oracle/_ref/."""
+    """Builds the CPU oracle (test infrastructure: the checker and its timing
+    build) and, when the reference tree is present, the reference harness into
+    oracle/_ref/."""
     odir = os.path.join(ROOT, "oracle")
-    subprocess.run(["make", "-s", "-C", odir, "-B", "liboracle.so"], check=True)
+    subprocess.run(["make", "-s", "-C", odir, "-B", "liboracle.so", "liboracle_bench.so"], check=True)
     if with_reference and os.path.isdir("/root/reference/cpp"):
         subprocess.run(["make", "-s", "-C", odir, "-B", "ref"], check=True)
 

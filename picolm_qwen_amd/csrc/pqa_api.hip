@@ -38,6 +38,7 @@ static void free_ctx(pqa_ctx* c) {
                     c->part_ml,   c->stage,     c->qkv};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    if (c->hstage) (void)hipHostFree(c->hstage);
     for (int i = 0; i < 2; ++i) {
         if (c->kvc_buf[i]) (void)hipHostFree(c->kvc_buf[i]);
         if (c->kvc_ev[i]) (void)hipEventDestroy(c->kvc_ev[i]);
@@ -211,26 +212,62 @@ static int ensure_stage(pqa_ctx* ctx, size_t floats) {
     return PQA_OK;
 }
 
+// Payloads (q, k, v in and out back) up to this size go through one pinned
+// host buffer: a CPU copy into it, one host-to-device copy, the kernels, one
+// device-to-host copy. A decode call moves 2 (q_dim + kv_dim) floats, 80 KB at
+// 32 query heads of 128; every pageable copy would cost a staged transfer of
+// its own. Larger payloads (prompts) copy straight from the caller's memory,
+// where the runtime pipelines its own staging.
+constexpr size_t kHostStageBytes = size_t(4) << 20;
+
+static int ensure_hstage(pqa_ctx* ctx, size_t floats) {
+    if (floats <= ctx->hstage_floats) return PQA_OK;
+    if (ctx->hstage) (void)hipHostFree(ctx->hstage);
+    ctx->hstage = nullptr;
+    ctx->hstage_floats = 0;
+    if (int rc = hip_check(ctx, hipHostMalloc((void**)&ctx->hstage, floats * sizeof(float), hipHostMallocDefault),
+                           "pinned staging"))
+        return rc;
+    ctx->hstage_floats = floats;
+    return PQA_OK;
+}
+
 static int run_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, const float* q, const float* k,
                     const float* v, float* out, const char* fn) {
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": NULL buffer");
     if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": n_tok must be positive");
     const size_t nq = (size_t)n_tok * ctx->q_dim, nkv = (size_t)n_tok * ctx->kv_dim;
-    if (int rc = ensure_stage(ctx, 2 * nq + 2 * nkv)) return rc;
-    float* dq = ctx->stage;
+    const size_t in_floats = nq + 2 * nkv;
+    if (int rc = ensure_stage(ctx, in_floats + nq)) return rc;
+    float* dq = ctx->stage;  // q, k, v contiguous, then out
     float* dk = dq + nq;
     float* dv = dk + nkv;
     float* dout = dv + nkv;
     hipStream_t st = ctx->stream;
-    int rc = hip_check(ctx, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, st), fn);
-    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, st), fn);
-    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dv, v, nkv * 4, hipMemcpyHostToDevice, st), fn);
+    const bool pinned = (in_floats + nq) * sizeof(float) <= kHostStageBytes;
+    int rc = PQA_OK;
+    if (pinned) {
+        // the previous call ended with a stream sync, so the buffer is free
+        if ((rc = ensure_hstage(ctx, in_floats + nq))) return rc;
+        float* h = ctx->hstage;
+        std::memcpy(h, q, nq * sizeof(float));
+        std::memcpy(h + nq, k, nkv * sizeof(float));
+        std::memcpy(h + nq + nkv, v, nkv * sizeof(float));
+        rc = hip_check(ctx, hipMemcpyAsync(dq, h, in_floats * sizeof(float), hipMemcpyHostToDevice, st), fn);
+    } else {
+        rc = hip_check(ctx, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, st), fn);
+        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, st), fn);
+        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dv, v, nkv * 4, hipMemcpyHostToDevice, st), fn);
+    }
     if (!rc)
         rc = prefill ? pqa_prefill(ctx, layer, pos, n_tok, dq, dk, dv, dout)
                      : pqa_decode(ctx, layer, pos, dq, dk, dv, dout);
-    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(out, dout, nq * 4, hipMemcpyDeviceToHost, st), fn);
+    float* back = pinned ? ctx->hstage + in_floats : out;
+    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(back, dout, nq * 4, hipMemcpyDeviceToHost, st), fn);
     if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
+    else if (pinned) (void)hipStreamSynchronize(st);  // a failed call leaves no copy reading the buffer
+    if (!rc && pinned) std::memcpy(out, back, nq * sizeof(float));
     return rc;
 }
 

@@ -68,9 +68,13 @@ struct pqa_ctx {
     void* bsplit = nullptr;  // fp16 hi/lo operands of the batched GEMMs and their row scales
     size_t bsplit_bytes = 0;
 
-    // staging for the _host entry points
+    // staging for the _host entry points: device buffers for q, k, v and out,
+    // and a pinned host buffer that carries payloads up to kHostStageBytes in
+    // one copy each way
     float* stage = nullptr;
     size_t stage_floats = 0;
+    float* hstage = nullptr;
+    size_t hstage_floats = 0;
 
     // .kvc file streaming: two pinned host buffers and their copy events,
     // made on the first pqa_kvc_save / pqa_kvc_load
