@@ -185,12 +185,13 @@ __device__ __forceinline__ void lds_dma_b32(const void* base, unsigned voff, uns
 // ---- cross-lane exchanges without LDS round trips ----
 // DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
 // row_half_mirror (lane ^ 7 within 8), row_mirror (lane ^ 15 within 16),
-// row_ror:8 (lane ^ 8 within 16).
+// row_ror:8 (lane ^ 8 within 16), row_ror:4 (not an involution).
 constexpr int kDppXor1 = 0xB1;
 constexpr int kDppXor2 = 0x4E;
 constexpr int kDppXor7 = 0x141;
 constexpr int kDppXor15 = 0x140;
 constexpr int kDppXor8 = 0x128;
+constexpr int kDppRor4 = 0x124;  // row_ror:4: lane i of a 16-lane row reads lane (i + 4) mod 16
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
