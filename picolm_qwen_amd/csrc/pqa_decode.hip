@@ -27,10 +27,12 @@
 //   softmax each 16-lane group keeps its own running max / sum per head over
 //           the 4 rows of every tile that land in its registers; exp2; the
 //           accumulator is rescaled only when a maximum moves.
-//   PV      VALU (v_fma_mix): the same lane group loads those 4 V rows, each
-//           lane 8 head dims (HD/8 lanes per row), and accumulates
-//           p[row][h] * v for the G heads; p comes from lane h of the group by
-//           a DPP row broadcast.
+//   PV      whole-row workgroups (HBM-bound): VALU FMA; the same lane group
+//           loads those 4 V rows, each lane 8 head dims (HD/8 lanes per row),
+//           and accumulates p[row][h] * v for the G heads; p comes from lane h
+//           of the group by a DPP row broadcast.
+//           per-column workgroups (short histories, latency-bound): MFMA, see
+//           PVM below.
 // Lane groups are merged once per wave, waves of a column once per workgroup
 // (log-sum-exp weights); the workgroup writes the output (one split) or its
 // partial (max, sum, acc) per head, and decode_combine_kernel merges splits.
@@ -100,7 +102,14 @@ constexpr int kCombineDims = 16;  // head dims per combine workgroup (HD / 16 wo
 constexpr int kMaxCombineSplits = 256;
 constexpr int kShortRowsPerWave = 16;  // per-column workgroups: history rows per wave (one tile)
 
-template <int HD, int G>
+// PVM: PV on MFMA (v_mfma_f32_16x16x16_f16). The score tile S[row][head] that
+// the score MFMA leaves in lane (g, n), registers r = rows 4g + r of head n, is
+// exactly the B operand P[rows 4g..4g+3][head n] of the 16x16x16 product
+// O^T[dim][head] += V^T[dim][row] P[row][head]; V^T comes from a wave-private
+// LDS copy of the tile by transposing reads (ds_read_b64_tr_b16). The softmax
+// max then has to be common to the four lane groups (one max per head and
+// tile), and each wave's O is complete: no lane-group merge after the loop.
+template <int HD, int G, bool PVM>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
     constexpr int NW = kDecodeWaves;
     constexpr int NT = kDecodeTiles;
@@ -123,6 +132,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     __shared__ float s_new[NW][G];
     __shared__ float wm[NW][G];
     __shared__ float wl[NW][G];
+    // PVM: one V tile per wave, rows padded by 32 B so the four rows of a
+    // transposing read fall in distinct banks
+    constexpr int VSTR = 2 * HD + 32;
+    __shared__ __attribute__((aligned(16))) char s_vt[PVM ? NW : 1][PVM ? 16 * VSTR : 16];
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -292,14 +305,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 
     float m_run = NEG_INF;
     float l_run = 0.0f;
-    float acc[G][8];
+    constexpr int AG = PVM ? 1 : G;
+    float acc[AG][8];
 #pragma unroll
-    for (int h = 0; h < G; h++)
+    for (int h = 0; h < AG; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
+    constexpr int NM = HD / 16;  // PVM: 16-dim blocks of O^T
+    floatx4 o[PVM ? NM : 1];
+#pragma unroll
+    for (int m = 0; m < (PVM ? NM : 1); m++) o[m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // PVM: this lane's V row pieces in the staged tile, and its transposing-read
+    // address (row 4 grp + n / 4, dims 4 (n % 4) .. +3 of each 16-dim block)
+    char* vst = s_vt[PVM ? w : 0];
+    const int tr_off = (4 * grp + (n >> 2)) * VSTR + 8 * (n & 3);
 
     if (w0 < w1) {
-        auto process = [&](int tb, const u32x4 (&kf)[KS], const u32x4 (&vf)[VL]) {
+        auto scores = [&](int tb, const u32x4 (&kf)[KS], float (&s)[4]) {
             floatx4 S = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
@@ -307,49 +329,87 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
                 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[ks], S, 0, 0, 0);
                 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[ks], S, 0, 0, 0);
             }
-            float s[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) s[i] = (tb + 4 * grp + i < w1 && n < Gc) ? S[i] : NEG_INF;
-            const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            const float m_new = fmaxf(m_run, mx);
-            const bool moved = m_new > m_run;
-            if (__any(moved)) {
-                const float corr = moved ? fast_exp2(m_run - m_new) : 1.0f;
-                l_run *= corr;
-                m_run = m_new;
+        };
+        auto process = [&](int tb, const u32x4 (&kf)[KS], const u32x4 (&vf)[VL]) {
+            float s[4];
+            scores(tb, kf, s);
+            if constexpr (PVM) {
+                // stage the V tile (the previous tile's reads are done: one
+                // wave's LDS accesses execute in order)
 #pragma unroll
-                for (int h = 0; h < G; h++) {
-                    const float cf = row_bcast(corr, h);
+                for (int j = 0; j < VL; j++)
+                    *(u32x4*)(vst + (4 * grp + vsub + RPG * j) * VSTR + 2 * vdim) = vf[j];
+                // one max per head and tile: the four lane groups of head n
+                const float mx = max_x32(max_x16(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))));
+                const float m_new = fmaxf(m_run, mx);
+                const bool moved = m_new > m_run;
+                if (__any(moved)) {
+                    const float corr = moved ? fast_exp2(m_run - m_new) : 1.0f;
+                    l_run *= corr;
+                    m_run = m_new;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[h][e] *= cf;
+                    for (int m = 0; m < NM; m++) o[m] *= corr;
                 }
-            }
-            float p[4];
+                half4 pb;
+                float ls = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = s[i] == NEG_INF ? 0.0f : fast_exp2(s[i] - m_run);
-            l_run += (p[0] + p[1]) + (p[2] + p[3]);
+                for (int i = 0; i < 4; i++) {
+                    const _Float16 ph = (_Float16)(s[i] == NEG_INF ? 0.0f : fast_exp2(s[i] - m_run));
+                    pb[i] = ph;
+                    ls += (float)ph;  // the weights the product uses
+                }
+                l_run += ls;
+                wave_sync();
 #pragma unroll
-            for (int j = 0; j < VL; j++) {
-                const half8 vh = __builtin_bit_cast(half8, vf[j]);
-                float pr[G];
+                for (int m = 0; m < NM; m++) {
+                    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4v*)(vst + tr_off + 32 * m));
+                    o[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, raw), pb, o[m], 0, 0, 0);
+                }
+                wave_sync();
+            } else {
+                const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+                const float m_new = fmaxf(m_run, mx);
+                const bool moved = m_new > m_run;
+                if (__any(moved)) {
+                    const float corr = moved ? fast_exp2(m_run - m_new) : 1.0f;
+                    l_run *= corr;
+                    m_run = m_new;
 #pragma unroll
-                for (int h = 0; h < G; h++) {
-                    if constexpr (RPG == 1) {
-                        pr[h] = row_bcast(p[j], h);
-                    } else {
-                        const float lo = row_bcast(p[RPG * j], h), hi = row_bcast(p[RPG * j + 1], h);
-                        pr[h] = vsub ? hi : lo;
+                    for (int h = 0; h < AG; h++) {
+                        const float cf = row_bcast(corr, h);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[h][e] *= cf;
                     }
                 }
+                float p[4];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float ve = (float)vh[e];
+                for (int i = 0; i < 4; i++) p[i] = s[i] == NEG_INF ? 0.0f : fast_exp2(s[i] - m_run);
+                l_run += (p[0] + p[1]) + (p[2] + p[3]);
 #pragma unroll
-                    for (int h = 0; h < G; h++) acc[h][e] = fmaf(pr[h], ve, acc[h][e]);
+                for (int j = 0; j < VL; j++) {
+                    const half8 vh = __builtin_bit_cast(half8, vf[j]);
+                    float pr[AG];
+#pragma unroll
+                    for (int h = 0; h < AG; h++) {
+                        if constexpr (RPG == 1) {
+                            pr[h] = row_bcast(p[j], h);
+                        } else {
+                            const float lo = row_bcast(p[RPG * j], h), hi = row_bcast(p[RPG * j + 1], h);
+                            pr[h] = vsub ? hi : lo;
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float ve = (float)vh[e];
+#pragma unroll
+                        for (int h = 0; h < AG; h++) acc[h][e] = fmaf(pr[h], ve, acc[h][e]);
+                    }
                 }
             }
         };
-
         // Straight-line body: a tile past w1 (the second of the last pair) is
         // processed fully masked (its rows are clamped loads, its scores -inf,
         // so p = 0). A `break` here would give the compiler a path on which
@@ -373,12 +433,24 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     // ---------------- merge the four lane groups, then write the wave partial ----------------
     // Cross-lane sums by DPP / permlane swaps: lane groups differ in lane bits
     // 4 and 5; with HD 64 the two V rows of a lane group differ in bit 3.
-    {
+    if constexpr (PVM) {
+        // m_run is already common to the lane groups and O^T complete: sum l,
+        // store lane (g, n)'s O^T[16 m + 4 g + r][n] as head n's dims
+        const float l = sum_x32(sum_x16(l_run));
+        if (n < G) {
+#pragma unroll
+            for (int m = 0; m < NM; m++) *(floatx4*)(q_lds + n * QS + 16 * m + 4 * grp) = o[m];
+            if (grp == 0) {
+                wm[w][n] = m_run;
+                wl[w][n] = l;
+            }
+        }
+    } else {
         const float M = max_x32(max_x16(m_run));
         const float e = (m_run == NEG_INF) ? 0.0f : fast_exp2(m_run - M);
         const float l = sum_x32(sum_x16(l_run * e));
 #pragma unroll
-        for (int h = 0; h < G; h++) {
+        for (int h = 0; h < AG; h++) {
             const float eh = row_bcast(e, h);
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -389,7 +461,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
         }
         if (lane < LPR) {
 #pragma unroll
-            for (int h = 0; h < G; h++) {
+            for (int h = 0; h < AG; h++) {
                 float* dst = q_lds + h * QS + vdim;
                 *(float4*)dst = float4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
                 *(float4*)(dst + 4) = float4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
@@ -587,15 +659,29 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
     return PQA_OK;
 }
 
-template <int HD>
-static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
+// PV on MFMA for the per-column workgroups of short histories (7-8 query
+// heads per column made the VALU PV the bound there); whole-row workgroups
+// stream HBM and keep the VALU PV.
+constexpr bool kPvmShort = true;
+constexpr bool kPvmRows = false;
+
+template <int HD, bool PVM>
+static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
     switch (G) {
 #define PQA_CASE(GG) \
-    case GG: hipLaunchKernelGGL((decode_kernel<HD, GG>), grid, dim3(kDecodeThreads), 0, st, a); break;
+    case GG: hipLaunchKernelGGL((decode_kernel<HD, GG, PVM>), grid, dim3(kDecodeThreads), 0, st, a); break;
         PQA_CASE(1) PQA_CASE(2) PQA_CASE(3) PQA_CASE(4) PQA_CASE(5) PQA_CASE(6) PQA_CASE(7) PQA_CASE(8)
 #undef PQA_CASE
         default: return hipErrorInvalidValue;
     }
+    return hipSuccess;
+}
+
+template <int HD>
+static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
+    const hipError_t le = (a.cpw == 1 ? kPvmShort : kPvmRows) ? launch_decode_pv<HD, true>(a, G, grid, st)
+                                                              : launch_decode_pv<HD, false>(a, G, grid, st);
+    if (le != hipSuccess) return le;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
     if (a.nsplit > kMaxCombineSplits) return hipErrorInvalidValue;
