@@ -96,11 +96,11 @@ struct DecodeArgs {
 
 constexpr int kDecodeWaves = 8;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kDecodeTiles = 2;  // 16-row K/V tiles in flight per wave
+constexpr int kDecodeTiles = 2;  // whole-row workgroups: 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 16;  // head dims per combine workgroup (HD / 16 workgroups per head)
 constexpr int kMaxCombineSplits = 256;
-constexpr int kShortRowsPerWave = 16;  // per-column workgroups: history rows per wave (one tile)
+constexpr int kShortMaxTiles = 4;  // per-column workgroups: most tiles per wave (one split)
 
 // PVM: PV on MFMA (v_mfma_f32_16x16x16_f16). The score tile S[row][head] that
 // the score MFMA leaves in lane (g, n), registers r = rows 4g + r of head n, is
@@ -109,10 +109,11 @@ constexpr int kShortRowsPerWave = 16;  // per-column workgroups: history rows pe
 // LDS copy of the tile by transposing reads (ds_read_b64_tr_b16). The softmax
 // max then has to be common to the four lane groups (one max per head and
 // tile), and each wave's O is complete: no lane-group merge after the loop.
-template <int HD, int G, bool PVM>
+// NT: 16-row tiles in flight per wave. PF: the loop requests the tiles of its
+// next iteration (without it each wave runs one iteration of NT tiles).
+template <int HD, int G, bool PVM, int NT, bool PF>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
     constexpr int NW = kDecodeWaves;
-    constexpr int NT = kDecodeTiles;
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
     constexpr int LPR = HD / 8;       // lanes per V row (8 fp16 each)
     constexpr int VL = 4 * LPR / 16;  // V loads per lane per 16-row tile
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 #pragma unroll
             for (int b = 0; b < NT; b++) {
                 process(tb + 16 * b, kt[b], vt[b]);
-                load_tile(tb + 16 * (b + NT), kt[b], vt[b]);
+                if constexpr (PF) load_tile(tb + 16 * (b + NT), kt[b], vt[b]);
             }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -590,20 +591,35 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
     }
 }
 
-void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg) {
+void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg,
+                  int* tiles) {
     const int ny = ctx->n_kv_heads * ctx->n_chunk;
     if (ctx->split_override <= 0) {
-        // Short histories: one workgroup per column and split, its 8 waves on
-        // one 16-row tile each, so every wave's loads go out in one round trip
-        // and the splits merge in the combine launch; used while these
-        // workgroups fill at most a quarter of the CUs. (64 rows per wave, one
-        // split for C1, measured 14 % slower over the Qwen2.5-0.5B sweep.)
-        const int rps = kDecodeWaves * kShortRowsPerWave;
+        // Short histories: one workgroup per column and split. Up to 8 x 64
+        // rows the column is one split with 1, 2 or 4 tiles per wave, and the
+        // launch writes the output itself: no combine launch (C1 8.7 -> 7.3
+        // us). Four tiles go two in flight, two iterations: all four requested
+        // in the prologue measured 0.5 us slower at C1. Longer histories take
+        // one tile per wave, requested in the prologue, and splits merged by
+        // the combine launch (64 rows per wave there measured 10.5 against
+        // 9.1 us per layer over Qwen2.5-0.5B at ctx 1024-4096); used while
+        // these workgroups fill at most a quarter of the CUs.
+        if (hist <= kDecodeWaves * 16 * kShortMaxTiles) {
+            const int need = (hist + kDecodeWaves * 16 - 1) / (kDecodeWaves * 16);
+            const int nt = need <= 1 ? 1 : need <= 2 ? 2 : 4;
+            *rows_per_split = kDecodeWaves * 16 * nt;
+            *nsplit = 1;
+            *cols_per_wg = 1;
+            *tiles = nt;
+            return;
+        }
+        const int rps = kDecodeWaves * 16;
         const int ns = std::max(1, (hist + rps - 1) / rps);
         if (ns * ny <= ctx->cu_count / 4 && ns <= std::min(kMaxCombineSplits, max_splits)) {
             *rows_per_split = rps;
             *nsplit = ns;
             *cols_per_wg = 1;
+            *tiles = 1;
             return;
         }
     }
@@ -634,6 +650,7 @@ void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_sp
     *rows_per_split = rps;
     *nsplit = ns;
     *cols_per_wg = cols;
+    *tiles = kDecodeTiles;
 }
 
 int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
@@ -660,16 +677,14 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
 }
 
 // PV on MFMA for the per-column workgroups of short histories (7-8 query
-// heads per column made the VALU PV the bound there); whole-row workgroups
-// stream HBM and keep the VALU PV.
-constexpr bool kPvmShort = true;
-constexpr bool kPvmRows = false;
-
-template <int HD, bool PVM>
+// heads per column made the VALU PV the bound there), with 1, 2 or 4 tiles per
+// wave (4: two in flight, two iterations); whole-row workgroups stream HBM and
+// keep the VALU PV.
+template <int HD, bool PVM, int NT, bool PF>
 static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
     switch (G) {
 #define PQA_CASE(GG) \
-    case GG: hipLaunchKernelGGL((decode_kernel<HD, GG, PVM>), grid, dim3(kDecodeThreads), 0, st, a); break;
+    case GG: hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF>), grid, dim3(kDecodeThreads), 0, st, a); break;
         PQA_CASE(1) PQA_CASE(2) PQA_CASE(3) PQA_CASE(4) PQA_CASE(5) PQA_CASE(6) PQA_CASE(7) PQA_CASE(8)
 #undef PQA_CASE
         default: return hipErrorInvalidValue;
@@ -678,9 +693,12 @@ static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStr
 }
 
 template <int HD>
-static hipError_t launch_decode_hd(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
-    const hipError_t le = (a.cpw == 1 ? kPvmShort : kPvmRows) ? launch_decode_pv<HD, true>(a, G, grid, st)
-                                                              : launch_decode_pv<HD, false>(a, G, grid, st);
+static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 grid, hipStream_t st) {
+    hipError_t le = hipErrorInvalidValue;
+    if (a.cpw != 1) le = launch_decode_pv<HD, false, kDecodeTiles, true>(a, G, grid, st);
+    else if (tiles == 1) le = launch_decode_pv<HD, true, 1, false>(a, G, grid, st);
+    else if (tiles == 2) le = launch_decode_pv<HD, true, 2, false>(a, G, grid, st);
+    else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true>(a, G, grid, st);
     if (le != hipSuccess) return le;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
@@ -715,13 +733,14 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
     a.ny = ctx->n_kv_heads * ctx->n_chunk;
     a.rope = ctx->rope_style;
     a.kv_dim = (int)ctx->kv_dim;
-    decode_split(ctx, pos, ws.max_splits, &a.rows_per_split, &a.nsplit, &a.cpw);
+    int tiles = kDecodeTiles;
+    decode_split(ctx, pos, ws.max_splits, &a.rows_per_split, &a.nsplit, &a.cpw, &tiles);
     // One split writes the output itself; several write partials that
     // decode_combine_kernel merges in a second launch.
     a.qscale = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid(a.nsplit, (a.ny + a.cpw - 1) / a.cpw);
-    if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, grid, ctx->stream);
-    if (hd == 128) return launch_decode_hd<128>(a, ctx->chunk_heads, grid, ctx->stream);
+    if (hd == 64) return launch_decode_hd<64>(a, ctx->chunk_heads, tiles, grid, ctx->stream);
+    if (hd == 128) return launch_decode_hd<128>(a, ctx->chunk_heads, tiles, grid, ctx->stream);
     return hipErrorInvalidValue;
 }
 

@@ -91,9 +91,11 @@ namespace pqa {
 int set_err(pqa_ctx* ctx, int code, const std::string& msg);
 int hip_check(pqa_ctx* ctx, hipError_t e, const char* what);
 
-// Rows per decode workgroup, the number of splits (at most max_splits) and
-// the columns (KV head, chunk) per workgroup for `hist` history rows.
-void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg);
+// Rows per decode workgroup, the number of splits (at most max_splits), the
+// columns (KV head, chunk) per workgroup and the 16-row tiles per
+// wave for `hist` history rows.
+void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg,
+                  int* tiles);
 
 // Where a decode's split partials go: part_acc [ny][splits][G][hd] and
 // part_ml [ny][splits][G][2] floats, for at most max_splits splits.
