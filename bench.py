@@ -600,8 +600,8 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
     """The prompt path of a Qwen3-4B-shaped layer from the normed inputs
     (pqa_prefill_x): exact dequantization of Q4_K attn_q/attn_k and Q6_K
     attn_v, split into fp16 hi/lo parts (kept per layer after the first
-    call), one GEMM over 2048 tokens (rocBLAS, fp16 MFMA with fp32
-    accumulation), bias, then the K/V append and the causal MFMA prefill; 36
+    call), one GEMM over 2048 tokens (gemm_f16_nt_kernel, fp16 MFMA with
+    fp32 accumulation), bias, then the K/V append and the causal MFMA prefill; 36
     layers per step."""
     Q4K, Q6K = 13, 15
     cx = Ctx(n_layers, s, nh, nkv, hd, 0, 1e6)
@@ -761,7 +761,7 @@ def summarize_counters(dirs, match):
     if "SQ_VALU_MFMA_BUSY_CYCLES" in avg and "GRBM_GUI_ACTIVE" in avg:
         lines.append(f"mfma_busy_frac: {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / (avg['GRBM_GUI_ACTIVE'] / xcds * simds):.4f} "
                      f"(SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs): issued MFMA "
-                     f"cycles, the hi + lo q's second QK product included)")
+                     f"cycles; for the prefill, the hi + lo q's second QK product included)")
     if "SQ_VALU_MFMA_BUSY_CYCLES" in avg and "SQ_INSTS_MFMA" in avg and avg["SQ_INSTS_MFMA"]:
         lines.append(f"cycles_per_mfma: {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / avg['SQ_INSTS_MFMA']:.2f}")
     if "SQ_LDS_BANK_CONFLICT" in avg and "SQ_LDS_IDX_ACTIVE" in avg and avg["SQ_LDS_IDX_ACTIVE"]:
@@ -785,8 +785,8 @@ def summarize_trace(trace_dir):
         m = re.match(r"_ZN3pqa(\d+)", name)  # a name the tracer left mangled: pqa::<identifier>
         if m:
             name = "pqa::" + name[m.end():m.end() + int(m.group(1))]
-        # this library's kernels, and rocBLAS's GEMM kernels of the batched projections
-        if not name.startswith(("void pqa::", "pqa::", "Cijk_")):
+        # this library's kernels
+        if not name.startswith(("void pqa::", "pqa::")):
             continue
         grid = tuple(int(r.get(f"Grid_Size_{a}", r.get("Grid_Size", 0)) or 0) for a in "XYZ")
         g = groups.setdefault((name, grid), [])
@@ -794,8 +794,6 @@ def summarize_trace(trace_dir):
     lines = [f"{'kernel':52s} {'grid (threads)':>20s} {'calls':>7s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         short = name.replace("void pqa::", "").replace("pqa::", "").split("(")[0]
-        if short.startswith("Cijk_"):
-            short = "rocBLAS " + short[:40] + "..."
         lines.append(f"{short:52s} {str(grid):>20s} {len(d):7d} {sum(d) / len(d):9.2f} {min(d):9.2f} {max(d):9.2f}")
     return "\n".join(lines)
 

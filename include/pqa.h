@@ -221,8 +221,9 @@ int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float
  * Model::forward_batch, cpp/model.hpp:493-530) as one GEMM over all tokens
  * and all q/k/v rows: the GGUF weights are dequantized exactly
  * (dequantize_row_*); weights and inputs, each row scaled by a power of two,
- * are split into fp16 hi + lo parts (22 significand bits); the GEMM (rocBLAS,
- * fp16 MFMA, fp32 accumulation) sums w_hi x_hi + w_hi x_lo + w_lo x_hi; the
+ * are split into fp16 hi + lo parts (22 significand bits); the GEMM (this
+ * library's gemm_f16_nt_kernel, fp16 MFMA, fp32 accumulation) sums
+ * w_hi x_hi + w_hi x_lo + w_lo x_hi; the
  * scale is undone exactly and the bias added. The error stays within
  * (3 n_embd + 12) 2^-24 sum |w x|, so q/k/v agree with the reference to fp32
  * rounding (about 1e-6 relative), not bit for bit (pqa_qkv_project keeps the
@@ -231,8 +232,9 @@ int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float
  * Memory: the first call for a layer keeps that layer's split weights,
  * (q_dim + 2 kv_dim) * (6 n_embd + 4) bytes, until its weights are replaced
  * or the context is destroyed; the first call also allocates a q_dim * n_embd
- * float workspace and a rocBLAS handle, and each call needs a workspace of
- * n_tok * (6 n_embd + 4 (q_dim + 2 kv_dim) + 4) bytes, grown on demand.
+ * float workspace, and each call needs a workspace of about
+ * n_tok * (6 n_embd + 4 (q_dim + 2 kv_dim) + 4) bytes (rows padded to 64
+ * halfs), grown on demand.
  */
 int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k, float* v);
 

@@ -11,7 +11,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libpqa.so")
-SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip"]
+SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip",
+           "pqa_gemm.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: the K row written to the cache must round like the
@@ -36,8 +37,7 @@ def build(verbose: bool = False) -> str:
         with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
             list(ex.map(_compile, SOURCES, objs))
         tmp_lib = LIB + ".tmp"
-        # rocBLAS: the fp32 GEMMs of the batched projections (plain library GEMMs)
-        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp_lib, *objs, "-lrocblas"]
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp_lib, *objs]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -5,7 +5,8 @@
 // Each GGUF matrix is first dequantized into an fp32 workspace by the
 // expressions of dequantize_row_* (cpp/quant.hpp:176-281), exactly. Then
 // Y[n_tok][rows] = X[n_tok][n] W^T runs on the fp16 MFMA path with fp32
-// accumulation, as one GEMM over a K of 3n:
+// accumulation (gemm_f16_nt_kernel, pqa_gemm.hip), as one GEMM over a K of 3n
+// (rows padded with zeros to a multiple of 64):
 //   every row a of W and of X is scaled by a power of two 2^s (exact) so that
 //   max |a 2^s| lies in [2^14, 2^15), and split into hi = fp16(a 2^s) and
 //   lo = fp16(a 2^s - hi), which carry 22 of its 24 significand bits;
@@ -19,7 +20,6 @@
 // 1e-6 relative) rather than bit for bit. pqa_qkv_project keeps the
 // reference's order for one token.
 #include <hip/hip_fp16.h>
-#include <rocblas/rocblas.h>
 
 #include <string>
 
@@ -31,11 +31,13 @@ namespace pqa {
 __device__ __forceinline__ float bh2f(unsigned h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
 __device__ __forceinline__ unsigned bld16(const uint8_t* p) { return p[0] | ((unsigned)p[1] << 8); }
 
-// One thread per 32 elements of a row: dst[row][32 g .. 32 g + 31].
+// One thread per 32 elements of a row: dst[row][32 g .. 32 g + 31]. F32 and
+// F16 rows (block size 1) may end in a partial group; every other type's row
+// is whole 32-element groups.
 template <int T>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ w, int stride, int rows, int n,
                                                            float* __restrict__ dst) {
-    const int groups = n / 32;
+    const int groups = (n + 31) / 32;
     const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
     if (gid >= (long long)rows * groups) return;
     const int row = (int)(gid / groups), g = (int)(gid % groups);
@@ -43,9 +45,11 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     float* y = dst + (size_t)row * n + 32 * g;
     if constexpr (T == GG_F32) {
         const float* s = (const float*)(r + 128 * g);
-        for (int j = 0; j < 32; j++) y[j] = s[j];
+        const int cnt = min(32, n - 32 * g);
+        for (int j = 0; j < cnt; j++) y[j] = s[j];
     } else if constexpr (T == GG_F16) {
-        for (int j = 0; j < 32; j++) y[j] = bh2f(bld16(r + 64 * g + 2 * j));
+        const int cnt = min(32, n - 32 * g);
+        for (int j = 0; j < cnt; j++) y[j] = bh2f(bld16(r + 64 * g + 2 * j));
     } else if constexpr (T == GG_Q4_0) {  // d * ((float)nibble - 8)
         const uint8_t* b = r + 18 * g;
         const float d = bh2f(bld16(b));
@@ -99,12 +103,14 @@ __device__ __forceinline__ float split_max(float mx, float* s_max) {
 // mx in [2^e, 2^(e+1)): s = 14 - e; an all-zero row keeps s = 0
 __device__ __forceinline__ int split_shift(float mx) { return mx > 0.0f ? min(126, max(-126, 14 - ilogbf(mx))) : 0; }
 
+// dst rows are ld >= 3n halfs; halfs [3n, ld) are written as zeros.
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ src, int n, _Float16* __restrict__ dst,
-                                                     float* __restrict__ inv_scale, int x_layout) {
+                                                     int ld, float* __restrict__ inv_scale, int x_layout) {
     __shared__ float s_max[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float* a = src + (size_t)row * n;
-    _Float16* d = dst + (size_t)row * 3 * n;
+    _Float16* d = dst + (size_t)row * ld;
+    for (int i = 3 * n + tid; i < ld; i += 256) d[i] = (_Float16)0.0f;
     float mx = 0.0f;
     for (int i = tid; i < n; i += 256) mx = fmaxf(mx, fabsf(a[i]));
     mx = split_max(mx, s_max);
@@ -126,13 +132,14 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ s
 // half4s (same arithmetic, same bits).
 constexpr int kSplitVec = 8;
 __global__ __launch_bounds__(256) void split3_vec_kernel(const float* __restrict__ src, int n,
-                                                         _Float16* __restrict__ dst, float* __restrict__ inv_scale,
-                                                         int x_layout) {
+                                                         _Float16* __restrict__ dst, int ld,
+                                                         float* __restrict__ inv_scale, int x_layout) {
     __shared__ float s_max[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const int n4 = n >> 2;
     const float4* a = (const float4*)(src + (size_t)row * n);
-    _Float16* d = dst + (size_t)row * 3 * n;
+    _Float16* d = dst + (size_t)row * ld;
+    for (int i = 3 * n + tid; i < ld; i += 256) d[i] = (_Float16)0.0f;
     float4 v[kSplitVec];
     float mx = 0.0f;
 #pragma unroll
@@ -162,15 +169,18 @@ __global__ __launch_bounds__(256) void split3_vec_kernel(const float* __restrict
     }
 }
 
-// one workgroup per row of src [rows][n] into dst [rows][3n]
-static void launch_split3(const float* src, int rows, int n, _Float16* dst, float* inv_scale, int x_layout,
+// one workgroup per row of src [rows][n] into dst [rows][ld], ld = k_pad(n)
+static void launch_split3(const float* src, int rows, int n, _Float16* dst, int ld, float* inv_scale, int x_layout,
                           hipStream_t stream) {
     const bool vec = n % 4 == 0 && n <= 256 * 4 * kSplitVec && ((uintptr_t)src & 15) == 0;
     if (vec)
-        hipLaunchKernelGGL(split3_vec_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, inv_scale, x_layout);
+        hipLaunchKernelGGL(split3_vec_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, ld, inv_scale, x_layout);
     else
-        hipLaunchKernelGGL(split3_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, inv_scale, x_layout);
+        hipLaunchKernelGGL(split3_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, ld, inv_scale, x_layout);
 }
+
+// the GEMM's K: 3n rounded up to its 64-wide k tiles
+static int k_pad(int n) { return (3 * n + 63) / 64 * 64; }
 
 // The three outputs of the batched GEMM and their biases.
 struct ScatterArgs {
@@ -206,7 +216,7 @@ __global__ __launch_bounds__(256) void unscale_scatter_kernel(const float* __res
 }
 
 static hipError_t launch_dequant(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s) {
-    const long long items = (long long)rows * (n / 32);
+    const long long items = (long long)rows * ((n + 31) / 32);
     const dim3 grid((unsigned)((items + 255) / 256));
     switch (type) {
 #define PQA_DQ(T) \
@@ -223,19 +233,8 @@ static hipError_t launch_dequant(int type, const void* w, int stride, int rows, 
 using pqa::hip_check;
 using pqa::set_err;
 
-// The rocBLAS handle and the fp32 weight workspace of a context, made on the
-// first batched call.
+// The fp32 weight workspace of a context, made on the first batched call.
 static int ensure_batch(pqa_ctx* ctx, size_t wfloats, const char* fn) {
-    if (!ctx->blas) {
-        rocblas_handle h = nullptr;
-        if (rocblas_create_handle(&h) != rocblas_status_success)
-            return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": rocblas_create_handle failed");
-        if (rocblas_set_stream(h, ctx->stream) != rocblas_status_success) {
-            rocblas_destroy_handle(h);
-            return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": rocblas_set_stream failed");
-        }
-        ctx->blas = h;
-    }
     if (wfloats > ctx->wf32_floats) {
         if (ctx->wf32) (void)hipFree(ctx->wf32);
         ctx->wf32 = nullptr;
@@ -247,8 +246,6 @@ static int ensure_batch(pqa_ctx* ctx, size_t wfloats, const char* fn) {
 }
 
 void pqa_free_batch(pqa_ctx* c) {
-    if (c->blas) rocblas_destroy_handle((rocblas_handle)c->blas);
-    c->blas = nullptr;
     if (c->wf32) (void)hipFree(c->wf32);
     c->wf32 = nullptr;
     if (c->bsplit) (void)hipFree(c->bsplit);
@@ -259,15 +256,16 @@ void pqa_free_batch(pqa_ctx* c) {
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // A layer's W' = [hi | hi | lo] rows of attn_q, attn_k and attn_v, one after
-// the other ([total][3n] halfs), then their inverse scales: made once, on the
-// first batched call for the layer (dequantized through the fp32 workspace).
+// the other ([total][k_pad(n)] halfs), then their inverse scales: made once, on
+// the first batched call for the layer (dequantized through the fp32 workspace).
 static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     auto& p = ctx->proj[layer];
     if (p.split) return PQA_OK;
     const int n = p.n_embd;
     const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
-    const size_t wb = up256(total * 3 * n * 2);
+    const int kp = pqa::k_pad(n);
+    const size_t wb = up256(total * kp * 2);
     if (int rc = ensure_batch(ctx, ctx->q_dim * (size_t)n, fn)) return rc;
     void* buf = nullptr;
     if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256(total * 4)), fn)) return rc;
@@ -277,7 +275,7 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     for (int i = 0; i < 3; i++) {
         hipError_t e = pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
         if (e == hipSuccess) {
-            pqa::launch_split3((const float*)ctx->wf32, rows[i], n, w3 + off * 3 * n, w_inv + off, 0, ctx->stream);
+            pqa::launch_split3((const float*)ctx->wf32, rows[i], n, w3 + off * kp, kp, w_inv + off, 0, ctx->stream);
             e = hipGetLastError();
         }
         if (int rc = hip_check(ctx, e, fn)) {
@@ -290,8 +288,8 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     return PQA_OK;
 }
 
-// Per call: X' [n_tok][3n] halfs, the inverse scales of X's rows, and the
-// GEMM result Y [n_tok][total] floats.
+// Per call: X' [n_tok][k_pad(n)] halfs, the inverse scales of X's rows, and
+// the GEMM result Y [n_tok][total] floats.
 struct SplitBufs {
     _Float16* x3;
     float* x_inv;
@@ -299,7 +297,7 @@ struct SplitBufs {
 };
 
 static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs* sb, const char* fn) {
-    const size_t xb = up256((size_t)n_tok * 3 * n * 2), xs = up256((size_t)n_tok * 4);
+    const size_t xb = up256((size_t)n_tok * pqa::k_pad(n) * 2), xs = up256((size_t)n_tok * 4);
     const size_t need = xb + xs + (size_t)n_tok * total * 4;
     if (need > ctx->bsplit_bytes) {
         if (ctx->bsplit) (void)hipFree(ctx->bsplit);
@@ -323,20 +321,16 @@ static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, Split
     if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
+    const int kp = pqa::k_pad(n);
     const _Float16* w3 = (const _Float16*)p.split;
-    *w_inv = (const float*)((const char*)p.split + up256(total * 3 * n * 2));
+    *w_inv = (const float*)((const char*)p.split + up256(total * kp * 2));
     if (int rc = ensure_split(ctx, n_tok, n, total, sb, fn)) return rc;
-    pqa::launch_split3(xb, n_tok, n, sb->x3, sb->x_inv, 1, ctx->stream);
+    pqa::launch_split3(xb, n_tok, n, sb->x3, kp, sb->x_inv, 1, ctx->stream);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
-    // row-major Y[n_tok][total] = X'[n_tok][3n] W'[total][3n]^T, i.e.
-    // column-major C (total x n_tok) = W'^T (total x 3n) * X'^T (3n x n_tok)
-    const float one = 1.0f, zero = 0.0f;
-    if (rocblas_gemm_ex((rocblas_handle)ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (int)total, n_tok,
-                        3 * n, &one, w3, rocblas_datatype_f16_r, 3 * n, sb->x3, rocblas_datatype_f16_r, 3 * n, &zero,
-                        sb->y, rocblas_datatype_f32_r, (int)total, sb->y, rocblas_datatype_f32_r, (int)total,
-                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0) != rocblas_status_success)
-        return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": rocblas_gemm_ex failed");
-    return PQA_OK;
+    // Y[n_tok][total] = X'[n_tok][kp] W'[total][kp]^T
+    return hip_check(ctx,
+                     pqa::launch_gemm_f16_nt(sb->x3, kp, w3, kp, sb->y, (int)total, n_tok, (int)total, kp, ctx->stream),
+                     fn);
 }
 
 static int check_batch(pqa_ctx* ctx, int layer, int n_tok, const char* fn) {

@@ -59,10 +59,8 @@ struct pqa_ctx {
     std::vector<pqa_proj_weights> proj;
     float* qkv = nullptr;  // [q_dim + 2 kv_dim + q_dim]: q, k, v and the attention output
 
-    // batched projections (pqa_batch.hip): rocBLAS handle, fp32 weights of one
-    // matrix while a layer's split copy is made, and the per-call operands;
-    // made on first use
-    void* blas = nullptr;
+    // batched projections (pqa_batch.hip): fp32 weights of one matrix while a
+    // layer's split copy is made, and the per-call operands; made on first use
     float* wf32 = nullptr;
     size_t wf32_floats = 0;
     void* bsplit = nullptr;  // fp16 hi/lo operands of the batched GEMMs and their row scales
@@ -115,6 +113,10 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
 // context's device, or an error code with ctx->err set.
 int scratch_init(int device);
 int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn);
+// C[m][n] = sum_k A[m][k] B[n][k] (fp16 operands, fp32 result; k a multiple
+// of 64; pqa_gemm.hip).
+hipError_t launch_gemm_f16_nt(const _Float16* a, int lda, const _Float16* b, int ldb, float* c, int ldc, int m, int n,
+                              int k, hipStream_t stream);
 hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
                           const float* k, const float* v, float* out);
 // q/k/v of a prompt as the columns of one GEMM result y [n_tok][ld] (q at
@@ -139,5 +141,5 @@ hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float*
 // Frees every layer's projection weights (pqa_proj.hip).
 void pqa_free_projections(pqa_ctx* c);
 
-// Releases the rocBLAS handle and the fp32 weight workspace (pqa_batch.hip).
+// Releases the fp32 weight workspace and the batched operands (pqa_batch.hip).
 void pqa_free_batch(pqa_ctx* c);

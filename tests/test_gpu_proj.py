@@ -309,6 +309,30 @@ def test_batched_projection_follows_replaced_weights():
     att.close()
 
 
+def test_batched_projection_multi_tile_and_k_padding():
+    # the GEMM's edges: 600 tokens = 3 row blocks of 256 (the last partial),
+    # 640 output rows = 3 column blocks of 192 and a partial one, and F32
+    # weights of width 104 (K = 312 padded with zeros to 320); same bound
+    print("batched projection: multi-tile, padded K", flush=True)
+    rng = np.random.default_rng(6060)
+    nh, nkv, hd, dim, n_tok = 6, 2, 64, 104, 600
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    mats = [(make_rows(rng, O.GGUF_F32, rows, dim), make_bias(rng, O.GGUF_F32, rows)) for rows in
+            (nh * hd, nkv * hd, nkv * hd)]
+    att.set_qkv_weights(0, dim, mats[0][0], O.GGUF_F32, mats[1][0], O.GGUF_F32, mats[2][0], O.GGUF_F32,
+                        mats[0][1], O.GGUF_F32, mats[1][1], O.GGUF_F32, mats[2][1], O.GGUF_F32)
+    x = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    got = [g.cpu().numpy() for g in att.qkv_project_batch(0, torch.from_numpy(x).to(torch.device("cuda:0")))]
+    for name, g, (w, b) in zip("qkv", got, mats):
+        wf = np.stack([O.dequant_row(O.GGUF_F32, w[r], dim) for r in range(w.shape[0])]).astype(np.float64)
+        for t in sorted({0, 1, 255, 256, 300, 511, 512, 598, 599} | set(range(3, n_tok, 41))):
+            want = O.matmul_bias(x[t], w, O.GGUF_F32, w.shape[0], b, O.GGUF_F32)
+            mag = np.abs(wf) @ np.abs(x[t].astype(np.float64))
+            err = np.abs(g[t].astype(np.float64) - want)
+            assert np.all(err <= (4 * dim + 13) * 2.0 ** -24 * mag + 1e-30), (name, t, float(np.max(err)))
+    att.close()
+
+
 def test_prompt_path_from_xb_with_biases():
     # Qwen2.5-style layer: q/k/v biases (F32 and F16), no QK-norm, hd 64,
     # a prompt continuing at position 40; the prefill kernels read the scaled
