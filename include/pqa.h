@@ -243,6 +243,32 @@ int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, f
  * pointers xb [n_tok][n_embd], out [n_tok][n_heads*head_dim]. */
 int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* out);
 
+/* Output projection and residual for a whole prompt: x[t] += Wo attn[t] + bo
+ * for t < n_tok (the per-token matmul_bias + vec_add of Model::forward_batch,
+ * cpp/model.hpp:595-600), on the split fp16 GEMM of pqa_qkv_project_batch:
+ * the same error bound, (3 q_dim + 12) 2^-24 sum |w a|, not bit for bit
+ * (pqa_out_project keeps the order for one token). DEVICE pointers attn
+ * [n_tok][q_dim] and x [n_tok][n_embd] (16-byte aligned, n_embd a multiple of
+ * 4); asynchronous. The first call for a layer keeps its split attn_output
+ * rows, n_embd * (6 q_dim + 4) bytes, until they are replaced. */
+int pqa_out_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* attn, float* x);
+
+/* The attention half of one layer of Model::forward_batch for a prompt chunk,
+ * cpp/model.hpp:493-600 without the FFN: from the attention norm's output xb
+ * [n_tok][n_embd] to the residual stream x [n_tok][n_embd] (read and written),
+ * token i at position start_pos + i: pqa_prefill_x into a context workspace,
+ * then pqa_out_project_batch. Token i's attention reads only rows written by
+ * tokens <= i of the same layer, so the reference's token loop (norm, block,
+ * FFN per token) and this layer-at-once order give the same values. DEVICE
+ * pointers (x 16-byte aligned); asynchronous. */
+int pqa_prefill_block(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* x);
+
+/* pqa_attention_block (cpp/model.hpp:320-427) and pqa_prefill_block for HOST
+ * pointers, as a CPU forward loop holds xb and x in its RunState vectors: xb
+ * and x are copied in, x is copied back, the call synchronises. */
+int pqa_attention_block_host(pqa_ctx* ctx, int layer, int pos, const float* xb, float* x);
+int pqa_prefill_block_host(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* x);
+
 /* The context's HIP stream (a hipStream_t), for event timing or ordering. */
 void* pqa_stream(pqa_ctx* ctx);
 int pqa_sync(pqa_ctx* ctx);

@@ -47,6 +47,24 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+ADAPTER = os.path.join(PKG, "adapter")
+DEMO_LIB = os.path.join(ADAPTER, "libpqa_forward_demo.so")
+
+
+def build_adapter() -> str:
+    """Compiles adapter/forward_demo.cpp, the forward loops of include/pqa_forward.hpp
+    behind one C entry point, with g++ against libpqa.so (warnings are errors)."""
+    tmp_lib = DEMO_LIB + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fPIC", "-shared",
+           "-I" + os.path.join(ROOT, "include"), os.path.join(ADAPTER, "forward_demo.cpp"), "-o", tmp_lib,
+           "-L" + PKG, "-lpqa", "-Wl,-rpath,$ORIGIN/.."]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"adapter build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp_lib, DEMO_LIB)
+    return DEMO_LIB
+
+
 def build_oracle(with_reference: bool = True) -> None:
     """Builds the CPU oracle (test infrastructure: the checker and its timing
     build) and, when the reference tree is present, the reference harness into
@@ -59,4 +77,5 @@ def build_oracle(with_reference: bool = True) -> None:
 
 if __name__ == "__main__":
     build(verbose=True)
+    build_adapter()
     build_oracle()

@@ -25,6 +25,7 @@ EXPORTS = [
     "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_kvc_save", "pqa_kvc_load",
     "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x", "pqa_set_out_weights", "pqa_out_project",
     "pqa_attention_block", "pqa_qkv_project_batch", "pqa_prefill_x", "pqa_decode_noalloc",
+    "pqa_out_project_batch", "pqa_prefill_block", "pqa_attention_block_host", "pqa_prefill_block_host",
 ]
 
 
@@ -79,6 +80,10 @@ def lib() -> C.CDLL:
     L.pqa_attention_block.argtypes = [vp, i, i, vp, vp]
     L.pqa_qkv_project_batch.argtypes = [vp, i, i, vp, vp, vp, vp]
     L.pqa_prefill_x.argtypes = [vp, i, i, i, vp, vp]
+    L.pqa_out_project_batch.argtypes = [vp, i, i, vp, vp]
+    L.pqa_prefill_block.argtypes = [vp, i, i, i, vp, vp]
+    L.pqa_attention_block_host.argtypes = [vp, i, i, vp, vp]
+    L.pqa_prefill_block_host.argtypes = [vp, i, i, i, vp, vp]
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int

@@ -67,6 +67,14 @@ def _host(x, numel: int):
     return a
 
 
+def _host_inout(x, numel: int):
+    """A host array the library reads and updates in place (the residual stream)."""
+    if not (isinstance(x, np.ndarray) and x.dtype == np.float32 and x.flags.c_contiguous and x.flags.writeable
+            and x.size == numel):
+        raise ValueError(f"x must be a writeable C-contiguous float32 array of {numel} elements")
+    return x
+
+
 def _host_out(out, numel: int):
     """A host output array the library may write numel floats into."""
     if out is None:
@@ -324,7 +332,7 @@ class PicoAttention:
     @staticmethod
     def _tokens(xb, n_embd: int) -> int:
         """Token count of a [n_tok][n_embd] prompt input."""
-        if xb.dim() != 2 or int(xb.shape[1]) != n_embd:
+        if xb.ndim != 2 or int(xb.shape[1]) != n_embd:
             raise ValueError(f"expected xb of shape [n_tok][{n_embd}], got {tuple(xb.shape)}")
         if int(xb.shape[0]) <= 0:
             raise ValueError("n_tok must be positive")
@@ -378,8 +386,15 @@ class PicoAttention:
         return x
 
     def attention_block(self, layer: int, pos: int, xb, x):
-        """cpp/model.hpp:320-427 from the normed input xb: x += attn_output(attention(q, k, v))."""
+        """cpp/model.hpp:320-427 from the normed input xb: x += attn_output(attention(q, k, v)).
+        torch tensors on the device (x updated in place), or numpy arrays (the host
+        entry point; x updated in place)."""
         n, rows = self._embd(layer), self._outr(layer)
+        if not _is_torch(xb):
+            xh, hx = _host(xb, n), _host_inout(x, rows)
+            check(lib().pqa_attention_block_host(self.handle, layer, pos, xh.ctypes.data_as(C.c_void_p),
+                                                 hx.ctypes.data_as(C.c_void_p)), self.handle)
+            return x
         ptrs = (_dev_ptr(xb, "float32", n), _dev_ptr(x, "float32", rows))
         ext = self._enter(xb.device, (xb, x))
         check(lib().pqa_attention_block(self.handle, layer, pos, *ptrs), self.handle)
@@ -415,6 +430,36 @@ class PicoAttention:
         check(lib().pqa_prefill_x(self.handle, layer, start_pos, n_tok, *ptrs), self.handle)
         self._leave(xb.device, ext)
         return out
+
+    def out_project_batch(self, layer: int, attn, x):
+        """x[t] += Wo attn[t] + bo for a whole prompt (cpp/model.hpp:595-600), on the
+        split fp16 GEMM (within (3 q_dim + 12) 2^-24 sum |w a|); torch tensors on the
+        device, x [n_tok][n_embd] updated in place."""
+        rows = self._outr(layer)
+        n_tok = self._tokens(attn, self.q_dim)
+        ptrs = (_dev_ptr(attn, "float32", n_tok * self.q_dim), _dev_ptr(x, "float32", n_tok * rows))
+        ext = self._enter(attn.device, (attn, x))
+        check(lib().pqa_out_project_batch(self.handle, layer, n_tok, *ptrs), self.handle)
+        self._leave(attn.device, ext)
+        return x
+
+    def prefill_block(self, layer: int, start_pos: int, xb, x):
+        """The attention half of a forward_batch layer (cpp/model.hpp:493-600 without
+        the FFN): xb [n_tok][n_embd] (the attention norm's output) to the residual
+        stream x [n_tok][n_embd], updated in place. torch tensors on the device, or
+        numpy arrays (the host entry point)."""
+        n, rows = self._embd(layer), self._outr(layer)
+        n_tok = self._tokens(xb, n)
+        if not _is_torch(xb):
+            xh, hx = _host(xb, n_tok * n), _host_inout(x, n_tok * rows)
+            check(lib().pqa_prefill_block_host(self.handle, layer, start_pos, n_tok, xh.ctypes.data_as(C.c_void_p),
+                                               hx.ctypes.data_as(C.c_void_p)), self.handle)
+            return x
+        ptrs = (_dev_ptr(xb, "float32", n_tok * n), _dev_ptr(x, "float32", n_tok * rows))
+        ext = self._enter(xb.device, (xb, x))
+        check(lib().pqa_prefill_block(self.handle, layer, start_pos, n_tok, *ptrs), self.handle)
+        self._leave(xb.device, ext)
+        return x
 
     # -- .kvc persistence (picolm/model.c:870-983) ---------------------------
     def kvc_save(self, path: str, n_pos: int) -> None:

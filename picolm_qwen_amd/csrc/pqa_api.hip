@@ -271,6 +271,56 @@ static int run_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, c
     return rc;
 }
 
+// Host-pointer forms of pqa_attention_block and pqa_prefill_block: xb and x
+// (read and written) copied in, the block, x copied back, a stream sync; the
+// same pinned staging as run_host for payloads up to kHostStageBytes.
+static int run_block_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, const float* xb, float* x,
+                          const char* fn) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
+    if (int rc = check_layer(ctx, layer, fn)) return rc;
+    if (ctx->proj.empty() || !ctx->proj[layer].n_embd || !ctx->proj[layer].out_rows)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": the layer needs q/k/v and attn_output weights");
+    if (ctx->proj[layer].n_embd != ctx->proj[layer].out_rows)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": attn_q/k/v width and attn_output rows differ");
+    if (!xb || !x) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": NULL buffer");
+    if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": n_tok must be positive");
+    const size_t n = (size_t)n_tok * ctx->proj[layer].out_rows;
+    const size_t n4 = (n + 3) & ~(size_t)3;  // x starts 16-byte aligned in the staging
+    if (int rc = ensure_stage(ctx, n4 + n)) return rc;
+    float* dxb = ctx->stage;
+    float* dx = dxb + n4;
+    hipStream_t st = ctx->stream;
+    const bool pinned = (n4 + n + n) * sizeof(float) <= kHostStageBytes;
+    int rc = PQA_OK;
+    if (pinned) {
+        if ((rc = ensure_hstage(ctx, n4 + n + n))) return rc;
+        float* h = ctx->hstage;
+        std::memcpy(h, xb, n * sizeof(float));
+        std::memcpy(h + n4, x, n * sizeof(float));
+        rc = hip_check(ctx, hipMemcpyAsync(dxb, h, (n4 + n) * sizeof(float), hipMemcpyHostToDevice, st), fn);
+    } else {
+        rc = hip_check(ctx, hipMemcpyAsync(dxb, xb, n * sizeof(float), hipMemcpyHostToDevice, st), fn);
+        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dx, x, n * sizeof(float), hipMemcpyHostToDevice, st), fn);
+    }
+    if (!rc)
+        rc = prefill ? pqa_prefill_block(ctx, layer, pos, n_tok, dxb, dx) : pqa_attention_block(ctx, layer, pos, dxb, dx);
+    float* back = pinned ? ctx->hstage + n4 + n : x;
+    if (!rc) rc = hip_check(ctx, hipMemcpyAsync(back, dx, n * sizeof(float), hipMemcpyDeviceToHost, st), fn);
+    if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
+    else (void)hipStreamSynchronize(st);  // a failed call leaves no copy reading the buffers
+    if (!rc && pinned) std::memcpy(x, back, n * sizeof(float));
+    return rc;
+}
+
+extern "C" int pqa_attention_block_host(pqa_ctx* ctx, int layer, int pos, const float* xb, float* x) {
+    return run_block_host(ctx, layer, pos, 1, false, xb, x, "pqa_attention_block_host");
+}
+
+extern "C" int pqa_prefill_block_host(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb,
+                                      float* x) {
+    return run_block_host(ctx, layer, start_pos, n_tok, true, xb, x, "pqa_prefill_block_host");
+}
+
 extern "C" int pqa_decode_host(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
                                float* out) {
     return run_host(ctx, layer, pos, 1, false, q, k, v, out, "pqa_decode_host");

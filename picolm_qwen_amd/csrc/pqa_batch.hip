@@ -21,6 +21,7 @@
 // reference's order for one token.
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <string>
 
 #include "pqa_device.h"
@@ -215,6 +216,32 @@ __global__ __launch_bounds__(256) void unscale_scatter_kernel(const float* __res
     *(floatx4*)(a.out[m] + (size_t)t * a.rows[m] + rr) = o;
 }
 
+// The output projection of a prompt: Y [n_tok][rows] holds attn W_o^T scaled
+// by 2^(s_w + s_x); x[t][r] = x[t][r] + (Y[t][r] * 2^-(s_w + s_x) + b[r]),
+// the reference's matmul_bias then vec_add (cpp/model.hpp:595-600). Thread: 4
+// consecutive rows of one token (rows a multiple of 4).
+__global__ __launch_bounds__(256) void unscale_residual_kernel(const float* __restrict__ Y, int rows,
+                                                               const float* __restrict__ w_inv,
+                                                               const float* __restrict__ x_inv,
+                                                               const uint8_t* __restrict__ b, int btype,
+                                                               float* __restrict__ x) {
+    const int t = blockIdx.y;
+    const int r = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (r >= rows) return;
+    const floatx4 y = *(const floatx4*)(Y + (size_t)t * rows + r);
+    const floatx4 wi = *(const floatx4*)(w_inv + r);
+    const float xi = x_inv[t];
+    floatx4* xp = (floatx4*)(x + (size_t)t * rows + r);
+    floatx4 o = *xp;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float v = y[e] * (wi[e] * xi);
+        if (b) v = v + (btype == GG_F32 ? ((const float*)b)[r + e] : bh2f(bld16(b + 2 * (r + e))));
+        o[e] = o[e] + v;
+    }
+    *xp = o;
+}
+
 static hipError_t launch_dequant(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s) {
     const long long items = (long long)rows * ((n + 31) / 32);
     const dim3 grid((unsigned)((items + 255) / 256));
@@ -236,6 +263,8 @@ using pqa::set_err;
 // The fp32 weight workspace of a context, made on the first batched call.
 static int ensure_batch(pqa_ctx* ctx, size_t wfloats, const char* fn) {
     if (wfloats > ctx->wf32_floats) {
+        // earlier dequantizations on the stream may still write the old one
+        if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), fn)) return rc;
         if (ctx->wf32) (void)hipFree(ctx->wf32);
         ctx->wf32 = nullptr;
         ctx->wf32_floats = 0;
@@ -251,6 +280,9 @@ void pqa_free_batch(pqa_ctx* c) {
     if (c->bsplit) (void)hipFree(c->bsplit);
     c->bsplit = nullptr;
     c->bsplit_bytes = 0;
+    if (c->battn) (void)hipFree(c->battn);
+    c->battn = nullptr;
+    c->battn_floats = 0;
 }
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -258,6 +290,7 @@ static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 // A layer's W' = [hi | hi | lo] rows of attn_q, attn_k and attn_v, one after
 // the other ([total][k_pad(n)] halfs), then their inverse scales: made once, on
 // the first batched call for the layer (dequantized through the fp32 workspace).
+// The attn_output rows get the same form in out_split ([n_embd][k_pad(q_dim)]).
 static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     auto& p = ctx->proj[layer];
     if (p.split) return PQA_OK;
@@ -288,24 +321,56 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     return PQA_OK;
 }
 
+static int ensure_layer_out_split(pqa_ctx* ctx, int layer, const char* fn) {
+    auto& p = ctx->proj[layer];
+    if (p.out_split) return PQA_OK;
+    const int n = (int)ctx->q_dim, rows = p.out_rows;
+    const int kp = pqa::k_pad(n);
+    const size_t wb = up256((size_t)rows * kp * 2);
+    if (int rc = ensure_batch(ctx, (size_t)rows * n, fn)) return rc;
+    void* buf = nullptr;
+    if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256((size_t)rows * 4)), fn)) return rc;
+    hipError_t e = pqa::launch_dequant(p.wtype[3], p.w[3], p.stride[3], rows, n, ctx->wf32, ctx->stream);
+    if (e == hipSuccess) {
+        pqa::launch_split3((const float*)ctx->wf32, rows, n, (_Float16*)buf, kp, (float*)((char*)buf + wb), 0,
+                           ctx->stream);
+        e = hipGetLastError();
+    }
+    if (int rc = hip_check(ctx, e, fn)) {
+        (void)hipFree(buf);
+        return rc;
+    }
+    p.out_split = buf;
+    return PQA_OK;
+}
+
 // Per call: X' [n_tok][k_pad(n)] halfs, the inverse scales of X's rows, and
-// the GEMM result Y [n_tok][total] floats.
+// the GEMM result Y [n_tok][total] floats. The workspace grows on demand; work
+// queued earlier on the stream may still read the old one, so the stream is
+// drained before it is freed.
+static int grow_split(pqa_ctx* ctx, size_t need, const char* fn) {
+    if (need <= ctx->bsplit_bytes) return PQA_OK;
+    if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), fn)) return rc;
+    if (ctx->bsplit) (void)hipFree(ctx->bsplit);
+    ctx->bsplit = nullptr;
+    ctx->bsplit_bytes = 0;
+    if (int rc = hip_check(ctx, hipMalloc(&ctx->bsplit, need), fn)) return rc;
+    ctx->bsplit_bytes = need;
+    return PQA_OK;
+}
 struct SplitBufs {
     _Float16* x3;
     float* x_inv;
     float* y;
 };
 
+static size_t split_need(int n_tok, int n, size_t total) {
+    return up256((size_t)n_tok * pqa::k_pad(n) * 2) + up256((size_t)n_tok * 4) + (size_t)n_tok * total * 4;
+}
+
 static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs* sb, const char* fn) {
     const size_t xb = up256((size_t)n_tok * pqa::k_pad(n) * 2), xs = up256((size_t)n_tok * 4);
-    const size_t need = xb + xs + (size_t)n_tok * total * 4;
-    if (need > ctx->bsplit_bytes) {
-        if (ctx->bsplit) (void)hipFree(ctx->bsplit);
-        ctx->bsplit = nullptr;
-        ctx->bsplit_bytes = 0;
-        if (int rc = hip_check(ctx, hipMalloc(&ctx->bsplit, need), fn)) return rc;
-        ctx->bsplit_bytes = need;
-    }
+    if (int rc = grow_split(ctx, split_need(n_tok, n, total), fn)) return rc;
     char* base = (char*)ctx->bsplit;
     sb->x3 = (_Float16*)base;
     sb->x_inv = (float*)(base + xb);
@@ -395,3 +460,78 @@ extern "C" int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, 
     }
     return hip_check(ctx, pqa::launch_prefill_scaled(ctx, layer, start_pos, n_tok, ys, out), fn);
 }
+
+// The output projection of a whole prompt with the residual add, x[t] +=
+// attn[t] W_o^T + b for every token (the per-token matmul_bias + vec_add of
+// Model::forward_batch, cpp/model.hpp:595-600), on the same split fp16 GEMM as
+// the Q/K/V rows and within the same bound.
+static int out_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* attn, float* x, const char* fn) {
+    if (int rc = ensure_layer_out_split(ctx, layer, fn)) return rc;
+    const auto& p = ctx->proj[layer];
+    const int n = (int)ctx->q_dim, rows = p.out_rows;
+    const int kp = pqa::k_pad(n);
+    SplitBufs sb;
+    if (int rc = ensure_split(ctx, n_tok, n, (size_t)rows, &sb, fn)) return rc;
+    pqa::launch_split3(attn, n_tok, n, sb.x3, kp, sb.x_inv, 1, ctx->stream);
+    if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
+    const _Float16* w3 = (const _Float16*)p.out_split;
+    const float* w_inv = (const float*)((const char*)p.out_split + up256((size_t)rows * kp * 2));
+    if (int rc = hip_check(ctx, pqa::launch_gemm_f16_nt(sb.x3, kp, w3, kp, sb.y, rows, n_tok, rows, kp, ctx->stream),
+                           fn))
+        return rc;
+    const unsigned gx = (unsigned)((rows / 4 + 255) / 256);
+    hipLaunchKernelGGL(pqa::unscale_residual_kernel, dim3(gx, n_tok), dim3(256), 0, ctx->stream, (const float*)sb.y,
+                       rows, w_inv, (const float*)sb.x_inv, (const uint8_t*)p.b[3], p.btype[3], x);
+    return hip_check(ctx, hipGetLastError(), fn);
+}
+
+static int check_out_batch(pqa_ctx* ctx, int layer, int n_tok, const char* fn) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, std::string(fn) + ": ctx is NULL");
+    if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": bad layer");
+    if (ctx->proj.empty() || !ctx->proj[layer].out_rows)
+        return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": no attn_output weights for this layer");
+    if (n_tok <= 0) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": n_tok must be positive");
+    if (ctx->proj[layer].out_rows % 4)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED, std::string(fn) + ": n_embd must be a multiple of 4");
+    return PQA_OK;
+}
+
+extern "C" int pqa_out_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* attn, float* x) {
+    static const char* fn = "pqa_out_project_batch";
+    if (int rc = check_out_batch(ctx, layer, n_tok, fn)) return rc;
+    if (!attn || !x) return set_err(ctx, PQA_ERR_ARG, "pqa_out_project_batch: NULL buffer");
+    if (((uintptr_t)x & 15) != 0) return set_err(ctx, PQA_ERR_ARG, "pqa_out_project_batch: x must be 16-byte aligned");
+    return out_project_batch(ctx, layer, n_tok, attn, x, fn);
+}
+
+// The attention half of Model::forward_batch for one layer and a prompt chunk
+// (cpp/model.hpp:493-600 without the FFN): pqa_prefill_x into the context's
+// attention workspace, then pqa_out_project_batch into x.
+extern "C" int pqa_prefill_block(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* xb, float* x) {
+    static const char* fn = "pqa_prefill_block";
+    if (int rc = check_out_batch(ctx, layer, n_tok, fn)) return rc;
+    if (int rc = check_batch(ctx, layer, n_tok, fn)) return rc;
+    if (!xb || !x) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_block: NULL buffer");
+    if (((uintptr_t)x & 15) != 0) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_block: x must be 16-byte aligned");
+    if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
+        return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill_block: positions past max_seq_len");
+    // every buffer of both GEMMs exists before the first kernel is queued
+    const auto& p = ctx->proj[layer];
+    const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
+    const size_t need = std::max(split_need(n_tok, p.n_embd, total), split_need(n_tok, (int)ctx->q_dim, p.out_rows));
+    if (int rc = grow_split(ctx, need, fn)) return rc;
+    const size_t af = (size_t)n_tok * ctx->q_dim;
+    if (af > ctx->battn_floats) {
+        if (int rc = hip_check(ctx, hipStreamSynchronize(ctx->stream), fn)) return rc;
+        if (ctx->battn) (void)hipFree(ctx->battn);
+        ctx->battn = nullptr;
+        ctx->battn_floats = 0;
+        if (int rc = hip_check(ctx, hipMalloc(&ctx->battn, af * 4), fn)) return rc;
+        ctx->battn_floats = af;
+    }
+    if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
+    if (int rc = ensure_layer_out_split(ctx, layer, fn)) return rc;
+    if (int rc = pqa_prefill_x(ctx, layer, start_pos, n_tok, xb, ctx->battn)) return rc;
+    return out_project_batch(ctx, layer, n_tok, ctx->battn, x, fn);
+}
+

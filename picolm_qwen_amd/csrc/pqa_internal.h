@@ -27,6 +27,8 @@ struct pqa_proj_weights {
     // the batched path's fp16 hi/lo copy of the attn_q, attn_k and attn_v rows
     // and their row scales; made on the first batched call, dropped with the weights
     void* split = nullptr;
+    // the same for the attn_output rows (pqa_out_project_batch)
+    void* out_split = nullptr;
 };
 
 struct pqa_ctx {
@@ -65,6 +67,8 @@ struct pqa_ctx {
     size_t wf32_floats = 0;
     void* bsplit = nullptr;  // fp16 hi/lo operands of the batched GEMMs and their row scales
     size_t bsplit_bytes = 0;
+    float* battn = nullptr;  // pqa_prefill_block's attention rows [n_tok][q_dim]
+    size_t battn_floats = 0;
 
     // staging for the _host entry points: device buffers for q, k, v and out,
     // and a pinned host buffer that carries payloads up to kHostStageBytes in

@@ -406,6 +406,8 @@ void free_proj(pqa_ctx* c, int layer) {
     p.out_rows = 0;
     if (p.split) (void)hipFree(p.split);
     p.split = nullptr;
+    if (p.out_split) (void)hipFree(p.out_split);
+    p.out_split = nullptr;
 }
 
 }  // namespace
@@ -502,6 +504,8 @@ extern "C" int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
     if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
     auto& p = ctx->proj[layer];
     free_matrix(p, 3);
+    if (p.out_split) (void)hipFree(p.out_split);  // the batched path's copy of the old rows
+    p.out_split = nullptr;
     p.out_rows = 0;
     if (int rc = upload_matrix(ctx, p, 3, fn, width, n_embd, wo, wo_type, bo, bo_type)) {
         free_matrix(p, 3);
