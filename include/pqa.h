@@ -32,7 +32,7 @@ extern "C" {
 #define PQA_OK 0
 #define PQA_ERR_ARG (-1)         /* bad pointer, shape or layer index */
 #define PQA_ERR_RANGE (-2)       /* position outside [0, max_seq_len) */
-#define PQA_ERR_UNSUPPORTED (-3) /* head_dim not in {64, 128} */
+#define PQA_ERR_UNSUPPORTED (-3) /* a size the kernels do not take (head_dim odd or above 512, ...) */
 #define PQA_ERR_HIP (-4)         /* a HIP runtime call failed */
 #define PQA_ERR_NOMEM (-5)       /* device allocation failed */
 #define PQA_ERR_IO (-6)          /* a .kvc file could not be opened, read or written */
@@ -52,8 +52,12 @@ typedef enum {
  * Allocates the cache and uploads the RoPE tables. Replaces
  * Model::allocate_run_state's KV/RoPE part (cpp/model.hpp:1003-1017).
  * rope_cos/rope_sin: host, [max_seq_len][head_dim/2] (state.rope_cos/sin).
- * head_dim must be 64 or 128 and n_heads a multiple of n_kv_heads
- * (kv_mul, cpp/model.hpp:295). The cache starts zeroed, as the reference's
+ * head_dim must be even and at most 512 (the reference's acc[512],
+ * cpp/model.hpp:172) and n_heads a multiple of n_kv_heads (kv_mul,
+ * cpp/model.hpp:295). 64 and 128 run on the MFMA kernels; other sizes on
+ * plain VALU kernels with the same results contract (bit-exact K/V rows,
+ * outputs within max-abs 2e-3 / rel 1e-2), where q, k and v need only 4-byte
+ * and out 8-byte alignment. The cache starts zeroed, as the reference's
  * std::vector does.
  */
 int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_heads, int n_kv_heads,

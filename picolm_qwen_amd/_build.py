@@ -12,7 +12,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libpqa.so")
 SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip",
-           "pqa_gemm.hip"]
+           "pqa_gemm.hip", "pqa_general.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: the K row written to the cache must round like the

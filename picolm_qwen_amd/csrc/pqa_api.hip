@@ -35,7 +35,7 @@ static void free_ctx(pqa_ctx* c) {
     pqa_free_projections(c);
     pqa_free_batch(c);
     void* bufs[] = {c->key_cache, c->val_cache, c->rope_cos, c->rope_sin, c->qk_norm, c->part_acc,
-                    c->part_ml,   c->stage,     c->qkv};
+                    c->part_ml,   c->stage,     c->qkv,      c->gen_q};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->hstage) (void)hipHostFree(c->hstage);
@@ -60,8 +60,8 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
         return set_err(nullptr, PQA_ERR_ARG, "pqa_create: sizes must be positive");
     if (n_heads % n_kv_heads != 0)
         return set_err(nullptr, PQA_ERR_ARG, "pqa_create: n_heads must be a multiple of n_kv_heads");
-    if (head_dim != 64 && head_dim != 128)
-        return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: head_dim must be 64 or 128");
+    if (head_dim <= 0 || head_dim > pqa::kMaxHeadDim || head_dim % 2 != 0)
+        return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: head_dim must be even and at most 512");
     if (rope_style < 0 || rope_style > 2) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: bad rope_style");
     if (!rope_cos || !rope_sin) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: RoPE tables are NULL");
 
@@ -111,6 +111,7 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
     chk(dev_alloc(&c->part_acc, (size_t)ny * c->max_splits * c->chunk_heads * head_dim), "workspace");
     chk(dev_alloc(&c->part_ml, (size_t)ny * c->max_splits * c->chunk_heads * 2), "workspace");
     chk(dev_alloc(&c->qkv, 2 * c->q_dim + 2 * c->kv_dim), "workspace");
+    if (!pqa::mfma_head_dim(head_dim) && chk(dev_alloc(&c->gen_q, c->q_dim), "workspace")) c->gen_q_floats = c->q_dim;
     if (rc == PQA_OK) {
         // the no-allocation decode's scratch address on this device
         const int src = pqa::scratch_init(c->device);
@@ -131,8 +132,12 @@ extern "C" const char* pqa_last_error(const pqa_ctx* ctx) {
     return ctx ? ctx->err.c_str() : g_create_err.c_str();
 }
 
-static bool misaligned(const void* a, const void* b, const void* c, const void* d) {
-    return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d) & 15u) != 0;
+// The MFMA kernels move q, k, v and out as 16-byte vectors; the general
+// head_dim kernels read q, k and v as floats and write out as float pairs.
+static bool misaligned(const pqa_ctx* ctx, const void* a, const void* b, const void* c, const void* out) {
+    if (!pqa::mfma_head_dim(ctx->head_dim)) return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 3u) != 0 ||
+                                                   ((uintptr_t)out & 7u) != 0;
+    return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)out) & 15u) != 0;
 }
 
 static int check_layer(pqa_ctx* ctx, int layer, const char* fn) {
@@ -167,7 +172,7 @@ extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, cons
     if (int rc = check_layer(ctx, layer, "pqa_decode")) return rc;
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: NULL buffer");
-    if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: buffers must be 16-byte aligned");
+    if (misaligned(ctx, q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: buffers must be 16-byte aligned");
     const pqa::DecodeWorkspace ws{ctx->part_acc, ctx->part_ml, ctx->max_splits};
     return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out, ws), "pqa_decode");
 }
@@ -182,7 +187,7 @@ extern "C" int pqa_decode_noalloc(pqa_ctx* ctx, int layer, int pos, const float*
     if (int rc = check_layer(ctx, layer, fn)) return rc;
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode_noalloc: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: NULL buffer");
-    if (misaligned(q, k, v, out))
+    if (misaligned(ctx, q, k, v, out))
         return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: buffers must be 16-byte aligned");
     pqa::DecodeWorkspace ws;
     if (int rc = pqa::scratch_workspace(ctx, &ws, fn)) return rc;
@@ -197,7 +202,7 @@ extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, co
     if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill: positions out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: NULL buffer");
-    if (misaligned(q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: buffers must be 16-byte aligned");
+    if (misaligned(ctx, q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: buffers must be 16-byte aligned");
     return hip_check(ctx, pqa::launch_prefill(ctx, layer, start_pos, n_tok, q, k, v, out), "pqa_prefill");
 }
 

@@ -413,6 +413,9 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
     if (int rc = check_batch(ctx, layer, n_tok, fn)) return rc;
     if (!xb || !q || !k || !v) return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: NULL buffer");
     // q/k/v are written as float4s
+    if (ctx->q_dim % 4 || ctx->kv_dim % 4)
+        return set_err(ctx, PQA_ERR_UNSUPPORTED,
+                       "pqa_qkv_project_batch: n_heads * head_dim and n_kv_heads * head_dim must be multiples of 4");
     if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) != 0)
         return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: q, k and v must be 16-byte aligned");
     SplitBufs sb;

@@ -711,6 +711,7 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 g
 
 hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
                          const float* v, float* out, const DecodeWorkspace& ws) {
+    if (!mfma_head_dim(ctx->head_dim)) return launch_decode_general(ctx, layer, pos, q, k, v, out, ws);
     DecodeArgs a;
     const int hd = ctx->head_dim;
     a.q = q;

@@ -70,6 +70,11 @@ struct pqa_ctx {
     float* battn = nullptr;  // pqa_prefill_block's attention rows [n_tok][q_dim]
     size_t battn_floats = 0;
 
+    // head sizes other than 64 and 128 (pqa_general.hip): the prepared q rows,
+    // one token's worth from context creation on, grown by prompts
+    float* gen_q = nullptr;
+    size_t gen_q_floats = 0;
+
     // staging for the _host entry points: device buffers for q, k, v and out,
     // and a pinned host buffer that carries payloads up to kHostStageBytes in
     // one copy each way
@@ -89,6 +94,10 @@ struct pqa_ctx {
 };
 
 namespace pqa {
+
+// head sizes with MFMA kernels; other even sizes up to 512 take pqa_general.hip
+inline bool mfma_head_dim(int hd) { return hd == 64 || hd == 128; }
+constexpr int kMaxHeadDim = 512;
 
 int set_err(pqa_ctx* ctx, int code, const std::string& msg);
 int hip_check(pqa_ctx* ctx, hipError_t e, const char* what);
@@ -135,6 +144,13 @@ struct PrefillScaled {
     int bt[3];
 };
 hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, const PrefillScaled& ys, float* out);
+// The general-head_dim path (pqa_general.hip): the same contracts as
+// launch_decode and launch_prefill / launch_prefill_scaled (ys non-null: q, k
+// and v read from the scaled GEMM result, q/k/v pointers unused).
+hipError_t launch_decode_general(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
+                                 float* out, const DecodeWorkspace& ws);
+hipError_t launch_prefill_general(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q, const float* k,
+                                  const float* v, const PrefillScaled* ys, float* out);
 hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
 hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
 hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);

@@ -716,7 +716,7 @@ hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const f
                           const float* k, const float* v, float* out) {
     if (ctx->head_dim == 64) return launch_prefill_hd<64, false>(ctx, layer, start, n_tok, q, k, v, out, nullptr);
     if (ctx->head_dim == 128) return launch_prefill_hd<128, false>(ctx, layer, start, n_tok, q, k, v, out, nullptr);
-    return hipErrorInvalidValue;
+    return launch_prefill_general(ctx, layer, start, n_tok, q, k, v, nullptr, out);
 }
 
 hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, const PrefillScaled& ys, float* out) {
@@ -724,7 +724,7 @@ hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, 
         return launch_prefill_hd<64, true>(ctx, layer, start, n_tok, nullptr, nullptr, nullptr, out, &ys);
     if (ctx->head_dim == 128)
         return launch_prefill_hd<128, true>(ctx, layer, start, n_tok, nullptr, nullptr, nullptr, out, &ys);
-    return hipErrorInvalidValue;
+    return launch_prefill_general(ctx, layer, start, n_tok, nullptr, nullptr, nullptr, &ys, out);
 }
 
 }  // namespace pqa

@@ -39,8 +39,10 @@ def test_create_rejects_bad_shapes_before_any_device_call():
     h = C.c_void_p()
     tab = np.zeros(64 * 48, np.float32)
     p = tab.ctypes.data_as(C.c_void_p)
-    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 96, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 514, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
     assert b"head_dim" in L.pqa_last_error(None)
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 95, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
+    assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 0, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
     assert L.pqa_create(C.byref(h), 1, 64, 6, 4, 64, 0, p, p) == _lib.PQA_ERR_ARG
     assert b"multiple" in L.pqa_last_error(None)
     assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 64, 3, p, p) == _lib.PQA_ERR_ARG
@@ -90,7 +92,7 @@ int main(void) {
     float tab[64 * 48] = {0};
     /* the reference's forward loop would create one context per model; a bad
        head_dim is refused before any device call */
-    int rc = pqa_create(&ctx, 1, 64, 8, 2, 96, PQA_ROPE_NEOX_HALF, tab, tab);
+    int rc = pqa_create(&ctx, 1, 64, 8, 2, 514, PQA_ROPE_NEOX_HALF, tab, tab);
     if (rc != PQA_ERR_UNSUPPORTED || ctx != NULL) return 1;
     if (!strstr(pqa_last_error(NULL), "head_dim")) return 2;
     if (pqa_decode(NULL, 0, 0, NULL, NULL, NULL, NULL) != PQA_ERR_ARG) return 3;

@@ -28,7 +28,7 @@ int main() {
     d.n_embd = 512;
     d.n_heads = 8;
     d.n_kv_heads = 2;
-    d.head_dim = 96;  // refused by pqa_create before any device call
+    d.head_dim = 514;  // above 512: refused by pqa_create before any device call
     d.max_seq_len = 16;
     try {
         pqa_fwd::Attention a(d);
@@ -64,7 +64,7 @@ def test_forward_header_compiles_and_reports_errors(tmp_path):
 
 def test_demo_library_is_built_and_reports_errors():
     assert os.path.exists(DEMO), "run __graft_entry__.build()"
-    m = Model(1, n_layers=1, head_dim=96)
+    m = Model(1, n_layers=1, head_dim=514)
     xp = np.zeros((2, m.n), np.float32)
     xd = np.zeros((1, m.n), np.float32)
     rc, msg = m.run_demo(xp, xd)
