@@ -9,10 +9,11 @@
 //                    K and V rounded to fp16 into the cache (bit-exact, like
 //                    the MFMA path's prologues), q scaled by log2(e)/sqrt(hd)
 //                    into a workspace;
-//   gen_attn_kernel  one wave per (token, KV head chunk, key range): 64 keys
+//   gen_attn8_kernel one wave per (token, KV head chunk, key range): 64 keys
 //                    per tile, one key per lane for the scores (each lane
 //                    walks its key's row), online softmax per query head, then
-//                    the tile's V rows with one fp16 pair per lane;
+//                    the tile's V rows in 16-byte chunks (head_dim a multiple
+//                    of 8; gen_attn_kernel, with 4-byte loads, takes the rest);
 //   gen_combine_kernel  merges the key ranges of a long decode.
 // These are plain VALU kernels: they stream the cache and have no MFMA or
 // LDS-tiled operand path, which is what the 64/128 kernels add.
@@ -279,35 +280,208 @@ __global__ __launch_bounds__(64 * kGenWaves) void gen_attn_kernel(const GenAttnA
     }
 }
 
+// head_dim a multiple of 8: 16-byte loads in both phases, more of them in
+// flight. Scores: lane = key, its row read 4 chunks at a time with the next 4
+// requested before the current ones are summed. PV: lane = (sub, chunk), sub
+// = lane / (hd / 8): each pass covers 64 / (hd / 8) keys, one 16-byte chunk of
+// a V row per lane, 4 passes requested at once; the subs' partial sums meet
+// in LDS after the last tile (in sub order).
+template <int QW>
+__global__ __launch_bounds__(64 * kGenWaves) void gen_attn8_kernel(const GenAttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float s_q[kGenWaves][kGenMaxG][QW];
+    __shared__ float s_p[kGenWaves][kGenMaxG][64];
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int item = blockIdx.x * kGenWaves + w;
+    if (item >= a.ny * a.n_tok * a.nsplit) return;  // whole wave; no workgroup barrier below
+    const int split = item % a.nsplit;
+    const int rest = item / a.nsplit;
+    const int t = rest % a.n_tok;
+    const int y = rest / a.n_tok;
+    const int kvh = y / a.nchunk, hc = y - kvh * a.nchunk;
+    const int Gc = min(a.G, a.g - hc * a.G);
+    const int h0 = kvh * a.g + hc * a.G;
+    const int hd = a.hd, nc = hd >> 3;
+    const int pos = a.start + t;
+    const int kbeg = split * a.rps;
+    const int kend = min(kbeg + a.rps, pos + 1);
+    const int kps = 64 / nc;                 // keys per PV pass
+    const int sub = lane / nc, ch = lane - sub * nc;
+    const bool pv_lane = sub < kps;
+    const int passes = (64 + kps - 1) / kps;
+
+    float(*q)[QW] = s_q[w];
+    for (int h = 0; h < Gc; h++)
+        for (int e = lane; e < hd; e += 64) q[h][e] = a.qp[((size_t)t * a.nh + h0 + h) * hd + e];
+    wave_sync();
+
+    float m[kGenMaxG], l[kGenMaxG], acc[kGenMaxG][8];
+#pragma unroll
+    for (int h = 0; h < kGenMaxG; h++) {
+        m[h] = NEG_INF;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
+    }
+    const uint16_t* kbase = a.kc + (size_t)kvh * hd;
+    const uint16_t* vbase = a.vc + (size_t)kvh * hd;
+    for (int k0 = kbeg; k0 < kend; k0 += 64) {
+        const int key = k0 + lane;
+        const bool valid = key < kend;
+        const u32x4* kr = (const u32x4*)(kbase + (size_t)(valid ? key : kbeg) * a.kv_dim);
+        float sc[kGenMaxG];
+#pragma unroll
+        for (int h = 0; h < kGenMaxG; h++) sc[h] = 0.0f;
+        u32x4 nb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) nb[i] = kr[min(i, nc - 1)];
+        for (int c0 = 0; c0 < nc; c0 += 4) {
+            u32x4 cb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) cb[i] = nb[i];
+            if (c0 + 4 < nc) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) nb[i] = kr[min(c0 + 4 + i, nc - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (c0 + i < nc) {
+                    float kf[8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        kf[2 * e] = f16_bits_to_f32((uint16_t)(cb[i][e] & 0xFFFFu));
+                        kf[2 * e + 1] = f16_bits_to_f32((uint16_t)(cb[i][e] >> 16));
+                    }
+#pragma unroll
+                    for (int h = 0; h < kGenMaxG; h++) {
+                        if (h < Gc) {
+                            const floatx4 q0 = *(const floatx4*)&q[h][8 * (c0 + i)];
+                            const floatx4 q1 = *(const floatx4*)&q[h][8 * (c0 + i) + 4];
+                            float s = sc[h];
+#pragma unroll
+                            for (int e = 0; e < 4; e++) s = fmaf(q0[e], kf[e], s);
+#pragma unroll
+                            for (int e = 0; e < 4; e++) s = fmaf(q1[e], kf[4 + e], s);
+                            sc[h] = s;
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kGenMaxG; h++) {
+            if (h < Gc) {
+                const float sv = valid ? sc[h] : NEG_INF;
+                const float mn = fmaxf(m[h], group_max<64>(sv));  // finite: the tile has a key
+                const float alpha = fast_exp2(m[h] - mn);          // 0 on the first tile
+                const float p = valid ? fast_exp2(sv - mn) : 0.0f;
+                l[h] = l[h] * alpha + group_sum<64>(p);
+                m[h] = mn;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[h][e] *= alpha;
+                s_p[w][h][lane] = p;
+            }
+        }
+        wave_sync();
+        if (pv_lane) {
+            for (int p0 = 0; p0 < passes; p0 += 4) {
+                u32x4 vb[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int j = min((p0 + u) * kps + sub, 63);
+                    const int row = min(k0 + j, kend - 1);  // keys past kend have p = 0
+                    vb[u] = ((const u32x4*)(vbase + (size_t)row * a.kv_dim))[ch];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int j = (p0 + u) * kps + sub;
+                    if (p0 + u < passes && j < 64) {
+                        float vf[8];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            vf[2 * e] = f16_bits_to_f32((uint16_t)(vb[u][e] & 0xFFFFu));
+                            vf[2 * e + 1] = f16_bits_to_f32((uint16_t)(vb[u][e] >> 16));
+                        }
+#pragma unroll
+                        for (int h = 0; h < kGenMaxG; h++) {
+                            if (h < Gc) {
+                                const float pj = s_p[w][h][j];
+#pragma unroll
+                                for (int e = 0; e < 8; e++) acc[h][e] = fmaf(pj, vf[e], acc[h][e]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        wave_sync();  // every lane has read this tile's P before the next tile writes it
+    }
+
+    // the subs' partial sums, in sub order, into the q rows (no longer read)
+    for (int s2 = 0; s2 < kps; s2++) {
+        if (sub == s2) {
+#pragma unroll
+            for (int h = 0; h < kGenMaxG; h++) {
+                if (h < Gc) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        float* d = &q[h][8 * ch + e];
+                        *d = s2 == 0 ? acc[h][e] : *d + acc[h][e];
+                    }
+                }
+            }
+        }
+        wave_sync();
+    }
+#pragma unroll
+    for (int h = 0; h < kGenMaxG; h++) {
+        if (h < Gc) {
+            if (a.nsplit == 1) {
+                const float inv = 1.0f / l[h];
+                float* o = a.out + ((size_t)t * a.nh + h0 + h) * hd;
+                for (int e = lane; e < hd; e += 64) o[e] = q[h][e] * inv;
+            } else {
+                const size_t slot = ((size_t)y * a.nsplit + split) * a.G + h;
+                float* o = a.part_acc + slot * hd;
+                for (int e = lane; e < hd; e += 64) o[e] = q[h][e];
+                if (lane == 0) *(float2*)(a.part_ml + slot * 2) = float2{m[h], l[h]};
+            }
+        }
+    }
+}
+
 // out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s over the key ranges of
 // one query head; grid (G, ny). An empty range has m = -inf, weight 0.
 __global__ __launch_bounds__(256) void gen_combine_kernel(const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml, float* __restrict__ out,
                                                           int G, int g, int nchunk, int nsplit, int hd) {
     __shared__ float s_w[kMaxGenSplits];
-    __shared__ float s_inv;
+    __shared__ float s_red[2][4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, y = blockIdx.y;
     const int kvh = y / nchunk, hc = y - kvh * nchunk;
-    if (h >= min(G, g - hc * G)) return;
+    if (h >= min(G, g - hc * G)) return;  // whole workgroup
     const float* pml = part_ml + ((size_t)y * nsplit * G + h) * 2;
-    if (threadIdx.x == 0) {
-        float M = -__builtin_huge_valf();
-        for (int s = 0; s < nsplit; s++) M = fmaxf(M, pml[(size_t)s * G * 2]);
-        float L = 0.0f;
-        for (int s = 0; s < nsplit; s++) {
-            const float wt = fast_exp2(pml[(size_t)s * G * 2] - M);
-            s_w[s] = wt;
-            L = L + wt * pml[(size_t)s * G * 2 + 1];
-        }
-        s_inv = 1.0f / L;
-    }
+    // thread s holds key range s (nsplit <= 256)
+    const float2 ml = tid < nsplit ? *(const float2*)(pml + (size_t)tid * G * 2)
+                                   : float2{-__builtin_huge_valf(), 0.0f};
+    float mx = group_max<64>(ml.x);
+    if (lane == 0) s_red[0][wv] = mx;
     __syncthreads();
-    const float inv = s_inv;
+    const float M = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+    const float wt = tid < nsplit ? fast_exp2(ml.x - M) : 0.0f;
+    if (tid < nsplit) s_w[tid] = wt;
+    const float wl = group_sum<64>(wt * ml.y);
+    if (lane == 0) s_red[1][wv] = wl;
+    __syncthreads();
+    const float inv = 1.0f / ((s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]));
     const float* pa = part_acc + ((size_t)y * nsplit * G + h) * hd;
     float* o = out + (size_t)(kvh * g + hc * G + h) * hd;
-    for (int d = threadIdx.x; d < hd; d += 256) {
+    for (int d = tid; d < hd; d += 256) {
         float acc = 0.0f;
-        for (int s = 0; s < nsplit; s++) acc = fmaf(s_w[s], pa[(size_t)s * G * hd + d], acc);
+#pragma unroll 8
+        for (int s2 = 0; s2 < nsplit; s2++) acc = fmaf(s_w[s2], pa[(size_t)s2 * G * hd + d], acc);
         o[d] = acc * inv;
     }
 }
@@ -355,9 +529,8 @@ static hipError_t launch_gen_prep(pqa_ctx* ctx, int layer, int start, int n_tok,
 }
 
 template <int NS>
-static hipError_t launch_gen_attn_ns(const GenAttnArgs& a, bool v8, dim3 grid, hipStream_t st) {
-    if (v8) hipLaunchKernelGGL((gen_attn_kernel<NS, 8>), grid, dim3(64 * kGenWaves), 0, st, a);
-    else hipLaunchKernelGGL((gen_attn_kernel<NS, 2>), grid, dim3(64 * kGenWaves), 0, st, a);
+static hipError_t launch_gen_attn_ns(const GenAttnArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((gen_attn_kernel<NS, 2>), grid, dim3(64 * kGenWaves), 0, st, a);
     return hipGetLastError();
 }
 
@@ -387,7 +560,7 @@ static hipError_t launch_gen_attn(pqa_ctx* ctx, int layer, int start, int n_tok,
         // all, at most the workspace's split count
         const int hist = start + 1;
         const int max_s = std::min(ws->max_splits, kMaxGenSplits);
-        const int target = std::max(1, std::min(max_s, 4 * ctx->cu_count / a.ny));
+        const int target = std::max(1, std::min(max_s, 8 * ctx->cu_count / a.ny));
         int rps = (hist + target - 1) / target;
         rps = std::max(64, (rps + 63) / 64 * 64);
         while ((hist + rps - 1) / rps > max_s) rps += 64;
@@ -396,12 +569,20 @@ static hipError_t launch_gen_attn(pqa_ctx* ctx, int layer, int start, int n_tok,
     }
     const long long items = (long long)a.ny * n_tok * a.nsplit;
     const dim3 grid((unsigned)((items + kGenWaves - 1) / kGenWaves));
-    const bool v8 = hd % 8 == 0;
-    const int ns = (hd / 2 + 63) / 64;
-    hipError_t e = ns == 1 ? launch_gen_attn_ns<1>(a, v8, grid, ctx->stream)
-                 : ns == 2 ? launch_gen_attn_ns<2>(a, v8, grid, ctx->stream)
-                 : ns == 3 ? launch_gen_attn_ns<3>(a, v8, grid, ctx->stream)
-                           : launch_gen_attn_ns<4>(a, v8, grid, ctx->stream);
+    hipError_t e;
+    if (hd % 8 == 0) {
+        const dim3 blk(64 * kGenWaves);
+        if (hd <= 128) hipLaunchKernelGGL(gen_attn8_kernel<128>, grid, blk, 0, ctx->stream, a);
+        else if (hd <= 256) hipLaunchKernelGGL(gen_attn8_kernel<256>, grid, blk, 0, ctx->stream, a);
+        else hipLaunchKernelGGL(gen_attn8_kernel<512>, grid, blk, 0, ctx->stream, a);
+        e = hipGetLastError();
+    } else {
+        const int ns = (hd / 2 + 63) / 64;
+        e = ns == 1 ? launch_gen_attn_ns<1>(a, grid, ctx->stream)
+          : ns == 2 ? launch_gen_attn_ns<2>(a, grid, ctx->stream)
+          : ns == 3 ? launch_gen_attn_ns<3>(a, grid, ctx->stream)
+                    : launch_gen_attn_ns<4>(a, grid, ctx->stream);
+    }
     if (e != hipSuccess || a.nsplit == 1) return e;
     hipLaunchKernelGGL(gen_combine_kernel, dim3(a.G, a.ny), dim3(256), 0, ctx->stream, (const float*)a.part_acc,
                        (const float*)a.part_ml, out, a.G, a.g, a.nchunk, a.nsplit, hd);
