@@ -600,7 +600,7 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
     """The prompt path of a Qwen3-4B-shaped layer from the normed inputs
     (pqa_prefill_x): exact dequantization of Q4_K attn_q/attn_k and Q6_K
     attn_v, split into fp16 hi/lo parts (kept per layer after the first
-    call), one GEMM over 2048 tokens (gemm_f16_nt_kernel, fp16 MFMA with
+    call), one GEMM over 2048 tokens (gemm_f16x3_nt_kernel, fp16 MFMA with
     fp32 accumulation), bias, then the K/V append and the causal MFMA prefill; 36
     layers per step."""
     Q4K, Q6K = 13, 15

@@ -226,7 +226,7 @@ int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float
  * and all q/k/v rows: the GGUF weights are dequantized exactly
  * (dequantize_row_*); weights and inputs, each row scaled by a power of two,
  * are split into fp16 hi + lo parts (22 significand bits); the GEMM (this
- * library's gemm_f16_nt_kernel, fp16 MFMA, fp32 accumulation) sums
+ * library's gemm_f16x3_nt_kernel, fp16 MFMA, fp32 accumulation) sums
  * w_hi x_hi + w_hi x_lo + w_lo x_hi; the
  * scale is undone exactly and the bias added. The error stays within
  * (3 n_embd + 12) 2^-24 sum |w x|, so q/k/v agree with the reference to fp32
@@ -234,11 +234,11 @@ int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float
  * order for one token). DEVICE pointers xb [n_tok][n_embd], q [n_tok][q_dim],
  * k and v [n_tok][kv_dim]; asynchronous on the context stream.
  * Memory: the first call for a layer keeps that layer's split weights,
- * (q_dim + 2 kv_dim) * (6 n_embd + 4) bytes, until its weights are replaced
- * or the context is destroyed; the first call also allocates a q_dim * n_embd
- * float workspace, and each call needs a workspace of about
- * n_tok * (6 n_embd + 4 (q_dim + 2 kv_dim) + 4) bytes (rows padded to 64
- * halfs), grown on demand.
+ * about (q_dim + 2 kv_dim) * (4 n_embd + 4) bytes, until its weights are
+ * replaced or the context is destroyed; the first call also allocates a
+ * q_dim * n_embd float workspace, and each call needs a workspace of about
+ * n_tok * (4 n_embd + 4 (q_dim + 2 kv_dim) + 4) bytes (the hi and lo halves
+ * of a row each padded to 32 halfs), grown on demand.
  */
 int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* q, float* k, float* v);
 
@@ -254,7 +254,7 @@ int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float
  * (pqa_out_project keeps the order for one token). DEVICE pointers attn
  * [n_tok][q_dim] and x [n_tok][n_embd] (16-byte aligned, n_embd a multiple of
  * 4); asynchronous. The first call for a layer keeps its split attn_output
- * rows, n_embd * (6 q_dim + 4) bytes, until they are replaced. */
+ * rows, about n_embd * (4 q_dim + 4) bytes, until they are replaced. */
 int pqa_out_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* attn, float* x);
 
 /* The attention half of one layer of Model::forward_batch for a prompt chunk,

@@ -5,20 +5,19 @@
 // Each GGUF matrix is first dequantized into an fp32 workspace by the
 // expressions of dequantize_row_* (cpp/quant.hpp:176-281), exactly. Then
 // Y[n_tok][rows] = X[n_tok][n] W^T runs on the fp16 MFMA path with fp32
-// accumulation (gemm_f16_nt_kernel, pqa_gemm.hip), as one GEMM over a K of 3n
-// (rows padded with zeros to a multiple of 64):
+// accumulation (gemm_f16x3_nt_kernel, pqa_gemm.hip):
 //   every row a of W and of X is scaled by a power of two 2^s (exact) so that
 //   max |a 2^s| lies in [2^14, 2^15), and split into hi = fp16(a 2^s) and
 //   lo = fp16(a 2^s - hi), which carry 22 of its 24 significand bits;
-//   W' = [hi | hi | lo] and X' = [hi | lo | hi] (each 3n halfs per row), so
-//   W' . X' = w_hi x_hi + w_hi x_lo + w_lo x_hi, dropping w_lo x_lo (about
-//   2^-22 of |w x|); fp16 products are exact in fp32;
+//   rows are stored as [hi | lo], each half padded with zeros to a multiple
+//   of 32, and the GEMM sums w_hi x_hi + w_hi x_lo + w_lo x_hi, dropping
+//   w_lo x_lo (about 2^-22 of |w x|); fp16 products are exact in fp32;
 //   the result is scaled back by 2^-(s_w + s_x) (exact), then the bias is
 //   added (vec_add: out + b).
 // The error stays within (3n + 12) 2^-24 sum |w x| for any summation order
-// the GEMM takes, so q/k/v agree with the reference to fp32 rounding (about
-// 1e-6 relative) rather than bit for bit. pqa_qkv_project keeps the
-// reference's order for one token.
+// the GEMM takes over its 3n products, so q/k/v agree with the reference to
+// fp32 rounding (about 1e-6 relative) rather than bit for bit.
+// pqa_qkv_project keeps the reference's order for one token.
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -91,8 +90,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
 }
 
 // One workgroup per row of n floats: max |a| over the row, the power of two
-// 2^s that takes it into [2^14, 2^15), dst row = the hi/lo halves of a 2^s in
-// the order [hi | hi | lo] (weights) or [hi | lo | hi] (inputs), and
+// 2^s that takes it into [2^14, 2^15), dst row = the hi and lo fp16 halves of
+// a 2^s as [hi | lo], each kh halfs wide (kh >= n, zeros past n), and
 // inv_scale[row] = 2^-s.
 __device__ __forceinline__ float split_max(float mx, float* s_max) {
     mx = group_max<64>(mx);
@@ -104,14 +103,16 @@ __device__ __forceinline__ float split_max(float mx, float* s_max) {
 // mx in [2^e, 2^(e+1)): s = 14 - e; an all-zero row keeps s = 0
 __device__ __forceinline__ int split_shift(float mx) { return mx > 0.0f ? min(126, max(-126, 14 - ilogbf(mx))) : 0; }
 
-// dst rows are ld >= 3n halfs; halfs [3n, ld) are written as zeros.
-__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ src, int n, _Float16* __restrict__ dst,
-                                                     int ld, float* __restrict__ inv_scale, int x_layout) {
+__global__ __launch_bounds__(256) void split2_kernel(const float* __restrict__ src, int n, _Float16* __restrict__ dst,
+                                                     int kh, float* __restrict__ inv_scale) {
     __shared__ float s_max[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float* a = src + (size_t)row * n;
-    _Float16* d = dst + (size_t)row * ld;
-    for (int i = 3 * n + tid; i < ld; i += 256) d[i] = (_Float16)0.0f;
+    _Float16* d = dst + (size_t)row * 2 * kh;
+    for (int i = n + tid; i < kh; i += 256) {
+        d[i] = (_Float16)0.0f;
+        d[kh + i] = (_Float16)0.0f;
+    }
     float mx = 0.0f;
     for (int i = tid; i < n; i += 256) mx = fmaxf(mx, fabsf(a[i]));
     mx = split_max(mx, s_max);
@@ -121,10 +122,8 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ s
     for (int i = tid; i < n; i += 256) {
         const float v = a[i] * sc;
         const _Float16 hi = (_Float16)v;
-        const _Float16 lo = (_Float16)(v - (float)hi);
         d[i] = hi;
-        d[n + i] = x_layout ? lo : hi;
-        d[2 * n + i] = x_layout ? hi : lo;
+        d[kh + i] = (_Float16)(v - (float)hi);
     }
 }
 
@@ -132,15 +131,18 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ s
 // aligned: the row is read once into registers as float4s and written as
 // half4s (same arithmetic, same bits).
 constexpr int kSplitVec = 8;
-__global__ __launch_bounds__(256) void split3_vec_kernel(const float* __restrict__ src, int n,
-                                                         _Float16* __restrict__ dst, int ld,
-                                                         float* __restrict__ inv_scale, int x_layout) {
+__global__ __launch_bounds__(256) void split2_vec_kernel(const float* __restrict__ src, int n,
+                                                         _Float16* __restrict__ dst, int kh,
+                                                         float* __restrict__ inv_scale) {
     __shared__ float s_max[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const int n4 = n >> 2;
     const float4* a = (const float4*)(src + (size_t)row * n);
-    _Float16* d = dst + (size_t)row * ld;
-    for (int i = 3 * n + tid; i < ld; i += 256) d[i] = (_Float16)0.0f;
+    _Float16* d = dst + (size_t)row * 2 * kh;
+    for (int i = n + tid; i < kh; i += 256) {
+        d[i] = (_Float16)0.0f;
+        d[kh + i] = (_Float16)0.0f;
+    }
     float4 v[kSplitVec];
     float mx = 0.0f;
 #pragma unroll
@@ -165,23 +167,22 @@ __global__ __launch_bounds__(256) void split3_vec_kernel(const float* __restrict
             lo[e] = (_Float16)(x[e] - (float)hi[e]);
         }
         *(half4*)(d + 4 * i) = hi;
-        *(half4*)(d + n + 4 * i) = x_layout ? lo : hi;
-        *(half4*)(d + 2 * n + 4 * i) = x_layout ? hi : lo;
+        *(half4*)(d + kh + 4 * i) = lo;
     }
 }
 
-// one workgroup per row of src [rows][n] into dst [rows][ld], ld = k_pad(n)
-static void launch_split3(const float* src, int rows, int n, _Float16* dst, int ld, float* inv_scale, int x_layout,
+// one workgroup per row of src [rows][n] into dst [rows][2 kh], kh = k_half(n)
+static void launch_split2(const float* src, int rows, int n, _Float16* dst, int kh, float* inv_scale,
                           hipStream_t stream) {
     const bool vec = n % 4 == 0 && n <= 256 * 4 * kSplitVec && ((uintptr_t)src & 15) == 0;
     if (vec)
-        hipLaunchKernelGGL(split3_vec_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, ld, inv_scale, x_layout);
+        hipLaunchKernelGGL(split2_vec_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, kh, inv_scale);
     else
-        hipLaunchKernelGGL(split3_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, ld, inv_scale, x_layout);
+        hipLaunchKernelGGL(split2_kernel, dim3(rows), dim3(256), 0, stream, src, n, dst, kh, inv_scale);
 }
 
-// the GEMM's K: 3n rounded up to its 64-wide k tiles
-static int k_pad(int n) { return (3 * n + 63) / 64 * 64; }
+// each half of a split row: n rounded up to the GEMM's 32-wide k tiles
+static int k_half(int n) { return (n + 31) / 32 * 32; }
 
 // The three outputs of the batched GEMM and their biases.
 struct ScatterArgs {
@@ -287,18 +288,18 @@ void pqa_free_batch(pqa_ctx* c) {
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// A layer's W' = [hi | hi | lo] rows of attn_q, attn_k and attn_v, one after
-// the other ([total][k_pad(n)] halfs), then their inverse scales: made once, on
+// A layer's W' = [hi | lo] rows of attn_q, attn_k and attn_v, one after the
+// other ([total][2 k_half(n)] halfs), then their inverse scales: made once, on
 // the first batched call for the layer (dequantized through the fp32 workspace).
-// The attn_output rows get the same form in out_split ([n_embd][k_pad(q_dim)]).
+// The attn_output rows get the same form in out_split ([n_embd][2 k_half(q_dim)]).
 static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     auto& p = ctx->proj[layer];
     if (p.split) return PQA_OK;
     const int n = p.n_embd;
     const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
-    const int kp = pqa::k_pad(n);
-    const size_t wb = up256(total * kp * 2);
+    const int kh = pqa::k_half(n);
+    const size_t wb = up256(total * 2 * kh * 2);
     if (int rc = ensure_batch(ctx, ctx->q_dim * (size_t)n, fn)) return rc;
     void* buf = nullptr;
     if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256(total * 4)), fn)) return rc;
@@ -308,7 +309,7 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     for (int i = 0; i < 3; i++) {
         hipError_t e = pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
         if (e == hipSuccess) {
-            pqa::launch_split3((const float*)ctx->wf32, rows[i], n, w3 + off * kp, kp, w_inv + off, 0, ctx->stream);
+            pqa::launch_split2((const float*)ctx->wf32, rows[i], n, w3 + off * 2 * kh, kh, w_inv + off, ctx->stream);
             e = hipGetLastError();
         }
         if (int rc = hip_check(ctx, e, fn)) {
@@ -325,14 +326,14 @@ static int ensure_layer_out_split(pqa_ctx* ctx, int layer, const char* fn) {
     auto& p = ctx->proj[layer];
     if (p.out_split) return PQA_OK;
     const int n = (int)ctx->q_dim, rows = p.out_rows;
-    const int kp = pqa::k_pad(n);
-    const size_t wb = up256((size_t)rows * kp * 2);
+    const int kh = pqa::k_half(n);
+    const size_t wb = up256((size_t)rows * 2 * kh * 2);
     if (int rc = ensure_batch(ctx, (size_t)rows * n, fn)) return rc;
     void* buf = nullptr;
     if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256((size_t)rows * 4)), fn)) return rc;
     hipError_t e = pqa::launch_dequant(p.wtype[3], p.w[3], p.stride[3], rows, n, ctx->wf32, ctx->stream);
     if (e == hipSuccess) {
-        pqa::launch_split3((const float*)ctx->wf32, rows, n, (_Float16*)buf, kp, (float*)((char*)buf + wb), 0,
+        pqa::launch_split2((const float*)ctx->wf32, rows, n, (_Float16*)buf, kh, (float*)((char*)buf + wb),
                            ctx->stream);
         e = hipGetLastError();
     }
@@ -344,7 +345,7 @@ static int ensure_layer_out_split(pqa_ctx* ctx, int layer, const char* fn) {
     return PQA_OK;
 }
 
-// Per call: X' [n_tok][k_pad(n)] halfs, the inverse scales of X's rows, and
+// Per call: X' [n_tok][2 k_half(n)] halfs, the inverse scales of X's rows, and
 // the GEMM result Y [n_tok][total] floats. The workspace grows on demand; work
 // queued earlier on the stream may still read the old one, so the stream is
 // drained before it is freed.
@@ -365,11 +366,11 @@ struct SplitBufs {
 };
 
 static size_t split_need(int n_tok, int n, size_t total) {
-    return up256((size_t)n_tok * pqa::k_pad(n) * 2) + up256((size_t)n_tok * 4) + (size_t)n_tok * total * 4;
+    return up256((size_t)n_tok * 2 * pqa::k_half(n) * 2) + up256((size_t)n_tok * 4) + (size_t)n_tok * total * 4;
 }
 
 static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs* sb, const char* fn) {
-    const size_t xb = up256((size_t)n_tok * pqa::k_pad(n) * 2), xs = up256((size_t)n_tok * 4);
+    const size_t xb = up256((size_t)n_tok * 2 * pqa::k_half(n) * 2), xs = up256((size_t)n_tok * 4);
     if (int rc = grow_split(ctx, split_need(n_tok, n, total), fn)) return rc;
     char* base = (char*)ctx->bsplit;
     sb->x3 = (_Float16*)base;
@@ -386,15 +387,16 @@ static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, Split
     if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
-    const int kp = pqa::k_pad(n);
+    const int kh = pqa::k_half(n);
     const _Float16* w3 = (const _Float16*)p.split;
-    *w_inv = (const float*)((const char*)p.split + up256(total * kp * 2));
+    *w_inv = (const float*)((const char*)p.split + up256(total * 2 * kh * 2));
     if (int rc = ensure_split(ctx, n_tok, n, total, sb, fn)) return rc;
-    pqa::launch_split3(xb, n_tok, n, sb->x3, kp, sb->x_inv, 1, ctx->stream);
+    pqa::launch_split2(xb, n_tok, n, sb->x3, kh, sb->x_inv, ctx->stream);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
-    // Y[n_tok][total] = X'[n_tok][kp] W'[total][kp]^T
+    // Y[n_tok][total] = X_hi W_hi^T + X_hi W_lo^T + X_lo W_hi^T
     return hip_check(ctx,
-                     pqa::launch_gemm_f16_nt(sb->x3, kp, w3, kp, sb->y, (int)total, n_tok, (int)total, kp, ctx->stream),
+                     pqa::launch_gemm_f16x3_nt(sb->x3, 2 * kh, w3, 2 * kh, sb->y, (int)total, n_tok, (int)total, kh,
+                                                        ctx->stream),
                      fn);
 }
 
@@ -472,14 +474,16 @@ static int out_project_batch(pqa_ctx* ctx, int layer, int n_tok, const float* at
     if (int rc = ensure_layer_out_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
     const int n = (int)ctx->q_dim, rows = p.out_rows;
-    const int kp = pqa::k_pad(n);
+    const int kh = pqa::k_half(n);
     SplitBufs sb;
     if (int rc = ensure_split(ctx, n_tok, n, (size_t)rows, &sb, fn)) return rc;
-    pqa::launch_split3(attn, n_tok, n, sb.x3, kp, sb.x_inv, 1, ctx->stream);
+    pqa::launch_split2(attn, n_tok, n, sb.x3, kh, sb.x_inv, ctx->stream);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
     const _Float16* w3 = (const _Float16*)p.out_split;
-    const float* w_inv = (const float*)((const char*)p.out_split + up256((size_t)rows * kp * 2));
-    if (int rc = hip_check(ctx, pqa::launch_gemm_f16_nt(sb.x3, kp, w3, kp, sb.y, rows, n_tok, rows, kp, ctx->stream),
+    const float* w_inv = (const float*)((const char*)p.out_split + up256((size_t)rows * 2 * kh * 2));
+    if (int rc = hip_check(ctx,
+                           pqa::launch_gemm_f16x3_nt(sb.x3, 2 * kh, w3, 2 * kh, sb.y, rows, n_tok, rows, kh,
+                                                     ctx->stream),
                            fn))
         return rc;
     const unsigned gx = (unsigned)((rows / 4 + 255) / 256);

@@ -126,10 +126,11 @@ hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const
 // context's device, or an error code with ctx->err set.
 int scratch_init(int device);
 int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn);
-// C[m][n] = sum_k A[m][k] B[n][k] (fp16 operands, fp32 result; k a multiple
-// of 64; pqa_gemm.hip).
-hipError_t launch_gemm_f16_nt(const _Float16* a, int lda, const _Float16* b, int ldb, float* c, int ldc, int m, int n,
-                              int k, hipStream_t stream);
+// C[m][n] = A_hi B_hi^T + A_hi B_lo^T + A_lo B_hi^T with rows of A (B) holding
+// hi at [0, kh) and lo at [kh, 2 kh) halfs (fp16 operands, fp32 result; kh a
+// multiple of 32; pqa_gemm.hip).
+hipError_t launch_gemm_f16x3_nt(const _Float16* a, int lda, const _Float16* b, int ldb, float* c, int ldc, int m,
+                                int n, int kh, hipStream_t stream);
 hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
                           const float* k, const float* v, float* out);
 // q/k/v of a prompt as the columns of one GEMM result y [n_tok][ld] (q at

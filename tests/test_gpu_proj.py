@@ -312,7 +312,7 @@ def test_batched_projection_follows_replaced_weights():
 def test_batched_projection_multi_tile_and_k_padding():
     # the GEMM's edges: 600 tokens = 3 row blocks of 256 (the last partial),
     # 640 output rows = 3 column blocks of 192 and a partial one, and F32
-    # weights of width 104 (K = 312 padded with zeros to 320); same bound
+    # weights of width 104 (each split half padded with zeros to 128); same bound
     print("batched projection: multi-tile, padded K", flush=True)
     rng = np.random.default_rng(6060)
     nh, nkv, hd, dim, n_tok = 6, 2, 64, 104, 600
