@@ -69,10 +69,10 @@ def prefill_flops(nh, hd, s, start=0):
 class Ctx:
     """Thin ctypes holder around one pqa context (the bench calls the C ABI directly)."""
 
-    def __init__(self, n_layers, smax, nh, nkv, hd, style, base):
+    def __init__(self, n_layers, smax, nh, nkv, hd, style, base, L=None):
         from picolm_qwen_amd import _lib
         from picolm_qwen_amd.attention import rope_table
-        self.L = _lib.lib()
+        self.L = L if L is not None else _lib.lib()
         self.check = _lib.check
         cos, sin = rope_table(base, hd, smax)
         h = C.c_void_p()
@@ -829,6 +829,67 @@ def secondary_workloads(torch, dev, steps, warmup, cpu_on):
     }
 
 
+# Phase stamps of the decode kernel (the stamped build, libpqa_stamps.so): slot
+# offsets as pqa_decode.hip numbers them, in s_memrealtime ticks (100 MHz).
+STAMP_SLOTS, STAMP_WGS = 64, 4096
+STAMP_PHASES = [("prologue loads issued", 1), ("q ready (norm, RoPE, LDS)", 10), ("history loop starts", 19),
+                ("history loop done", 28)]
+STAMP_MERGE, STAMP_END, STAMP_NEW0, STAMP_NEW1 = 37, 38, 39, 40
+
+
+def phase_stamps(cases=None, reps=7):
+    """Per-phase timings of single decode launches from the stamped build: for
+    each case, the median over reps launches of each wave's stamps relative to
+    its workgroup's start, averaged over workgroups (µs)."""
+    import torch
+    from picolm_qwen_amd import _lib
+    L = _lib.stamped_lib()
+    dev = torch.device("cuda:0")
+    cases = cases or [("tinyllama ctx 512 (32/4 heads, hd 64, block8)", 32, 4, 64, 1, 1e4, 511, False),
+                      ("qwen2.5-0.5b ctx 1 (14/2 heads, hd 64)", 14, 2, 64, 0, 1e6, 0, False),
+                      ("qwen2.5-0.5b ctx 301 (14/2 heads, hd 64)", 14, 2, 64, 0, 1e6, 300, False),
+                      ("qwen3 16/8 heads hd 128, ctx 201, QK-norm", 16, 8, 128, 0, 1e6, 200, True)]
+    lines = []
+    for name, nh, nkv, hd, style, base, pos, qk in cases:
+        cx = Ctx(1, pos + 1, nh, nkv, hd, style, base, L=L)
+        rng = np.random.default_rng(1)
+        if qk:
+            set_norms(cx, rng, hd)
+        if pos:
+            cx.check(L.pqa_synth_kv(cx.h, 0, 0, pos, 5, 0.0), cx.h)
+        q, k, v, out = make_inputs(torch, dev, rng, 1, 1, nh, nkv, hd)
+        torch.cuda.synchronize()
+        args = [C.c_void_p(t[0].data_ptr()) for t in (q, k, v, out)]
+        _, ev = timed(torch, cx, lambda: L.pqa_decode(cx.h, 0, pos, *args), 200, 20)
+        per = []
+        for _ in range(reps):
+            cx.check(L.pqa_decode_stamps_clear())
+            cx.check(L.pqa_decode(cx.h, 0, pos, *args), cx.h)
+            cx.check(L.pqa_sync(cx.h), cx.h)
+            a = np.zeros(STAMP_WGS * STAMP_SLOTS, np.uint64)
+            cx.check(L.pqa_decode_stamps_read(a.ctypes.data_as(C.c_void_p), a.size))
+            a = a.reshape(STAMP_WGS, STAMP_SLOTS).astype(np.int64)
+            a = a[a[:, 0] > 0]
+            rel = np.where(a > 0, (a - a[:, :1]) / 100.0, np.nan)
+            per.append((len(a), rel, (a[:, STAMP_END].max() - a[:, 0].min()) / 100.0))
+        nwg = per[0][0]
+        med = np.nanmedian(np.stack([np.nanmean(r, 0) for _, r, _ in per]), 0)
+        span = float(np.median([sp for _, _, sp in per]))
+        lines.append(f"{name}: {nwg} workgroup(s); {ev * 1e3:.2f} us per call event-timed (stamped build); "
+                     f"first start to last end {span:.2f} us")
+        lines.append("  us from the workgroup's start, per wave 0..8 (mean over workgroups, median of "
+                     f"{reps} launches; '  -  ': the wave has no such phase)")
+        for label, off in STAMP_PHASES:
+            lines.append(f"    {label:28s} " + " ".join("  -  " if np.isnan(x) else f"{x:5.2f}"
+                                                       for x in med[off:off + 9]))
+        lines.append(f"    {'writer wave: new row':28s} {med[STAMP_NEW0]:5.2f} -> {med[STAMP_NEW1]:5.2f}")
+        lines.append(f"    {'workgroup merge starts':28s} {med[STAMP_MERGE]:5.2f}")
+        lines.append(f"    {'outputs stored':28s} {med[STAMP_END]:5.2f}")
+        cx.close()
+        torch.cuda.empty_cache()
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -846,7 +907,12 @@ def main():
     ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_DIR",
                     help="per-dispatch counter averages of the kernels named by --kernel")
     ap.add_argument("--kernel", default="prefill_attn_kernel")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="per-phase decode timings from the stamped build (libpqa_stamps.so)")
     args = ap.parse_args()
+    if args.phase_stamps:
+        print(phase_stamps(), flush=True)
+        return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.kernel))
         return

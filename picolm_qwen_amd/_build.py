@@ -11,6 +11,9 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libpqa.so")
+# the same sources with -DPQA_PHASE_STAMPS: kernels also write s_memrealtime
+# stamps at their phase boundaries (measurement only, bench.py --phase-stamps)
+STAMPS_LIB = os.path.join(PKG, "libpqa_stamps.so")
 SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip",
            "pqa_gemm.hip", "pqa_general.hip"]
 
@@ -23,28 +26,31 @@ CFLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=
           "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 
 
-def _compile(src: str, obj: str) -> None:
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str, obj: str, extra=()) -> None:
+    cmd = [HIPCC, *CFLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every csrc/*.hip source and links libpqa.so; returns its path."""
+def build(verbose: bool = False, stamps: bool = False) -> str:
+    """Compiles every csrc/*.hip source and links libpqa.so (with stamps:
+    libpqa_stamps.so, the phase-stamped variant); returns its path."""
+    out = STAMPS_LIB if stamps else LIB
+    extra = ["-DPQA_PHASE_STAMPS"] if stamps else []
     with tempfile.TemporaryDirectory(prefix="pqa_build_") as tmp:
         objs = [os.path.join(tmp, s.replace(".hip", ".o")) for s in SOURCES]
         with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-            list(ex.map(_compile, SOURCES, objs))
-        tmp_lib = LIB + ".tmp"
+            list(ex.map(lambda s_o: _compile(*s_o, extra), zip(SOURCES, objs)))
+        tmp_lib = out + ".tmp"
         cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp_lib, *objs]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-        os.replace(tmp_lib, LIB)
+        os.replace(tmp_lib, out)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {out}")
+    return out
 
 
 ADAPTER = os.path.join(PKG, "adapter")
@@ -76,6 +82,11 @@ def build_oracle(with_reference: bool = True) -> None:
 
 
 if __name__ == "__main__":
+    import sys
+
+    if "--stamps" in sys.argv:
+        build(verbose=True, stamps=True)
+        sys.exit(0)
     build(verbose=True)
     build_adapter()
     build_oracle()

@@ -5,7 +5,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-from ._build import LIB
+from ._build import LIB, STAMPS_LIB
 
 PQA_OK = 0
 PQA_ERR_ARG = -1
@@ -36,15 +36,36 @@ class PQAError(RuntimeError):
 
 
 _lib = None
+_stamped = None
 
 
 def lib() -> C.CDLL:
     global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(LIB):
-        raise RuntimeError(f"{LIB} is not built; run __graft_entry__.build() (hipcc, gfx950)")
-    L = C.CDLL(LIB)
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+        _lib = _bind(C.CDLL(LIB))
+    return _lib
+
+
+def stamped_lib() -> C.CDLL:
+    """The phase-stamped build of the same sources (measurement only: its
+    kernels also write s_memrealtime stamps; pqa_decode_stamps_read and
+    pqa_decode_stamps_clear return them)."""
+    global _stamped
+    if _stamped is None:
+        if not os.path.exists(STAMPS_LIB):
+            raise RuntimeError(f"{STAMPS_LIB} is not built; run python -m picolm_qwen_amd._build --stamps")
+        L = _bind(C.CDLL(STAMPS_LIB))
+        L.pqa_decode_stamps_read.argtypes = [C.c_void_p, C.c_int]
+        L.pqa_decode_stamps_read.restype = C.c_int
+        L.pqa_decode_stamps_clear.argtypes = []
+        L.pqa_decode_stamps_clear.restype = C.c_int
+        _stamped = L
+    return _stamped
+
+
+def _bind(L: C.CDLL) -> C.CDLL:
     vp, i, f, u64, sz = C.c_void_p, C.c_int, C.c_float, C.c_uint64, C.c_size_t
     fp = C.POINTER(C.c_float)
     L.pqa_create.argtypes = [C.POINTER(vp), i, i, i, i, i, i, vp, vp]
@@ -87,7 +108,6 @@ def lib() -> C.CDLL:
     for name in EXPORTS:
         if name not in ("pqa_stream", "pqa_last_error", "pqa_destroy", "pqa_rope_table"):
             getattr(L, name).restype = C.c_int
-    _lib = L
     return L
 
 

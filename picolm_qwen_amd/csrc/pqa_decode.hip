@@ -75,6 +75,37 @@ int scratch_init(int device) {
     return PQA_OK;
 }
 
+// Phase stamps, compiled in only with -DPQA_PHASE_STAMPS (the build's
+// stamps=True variant, libpqa_stamps.so; bench.py --phase-stamps reads them):
+// s_memrealtime (a 100 MHz counter) at the phase boundaries of every wave,
+// kStampSlots per workgroup, read back by pqa_decode_stamps_read.
+constexpr int kStampSlots = 64;
+constexpr int kStampWGs = 4096;
+enum : int {
+    kStStart = 0,      // workgroup start (thread 0)
+    kStIssued = 1,     // + wave (up to 9 waves): prologue loads issued
+    kStQReady = 10,    // + wave: q normalised, rotated and in LDS
+    kStLoop0 = 19,     // + wave: history loop starts
+    kStLoop1 = 28,     // + wave: history loop done
+    kStMerge = 37,     // workgroup merge starts (after the barrier)
+    kStEnd = 38,       // outputs stored
+    kStNewRow0 = 39,   // the writer wave starts the new row
+    kStNewRow1 = 40,   // the writer wave has its score and V
+};
+#ifdef PQA_PHASE_STAMPS
+static __device__ unsigned long long g_decode_stamps[kStampWGs * kStampSlots];
+#define PQA_STAMP(slot, cond)                                                                          \
+    do {                                                                                               \
+        const unsigned wg_ = blockIdx.y * gridDim.x + blockIdx.x;                                      \
+        if ((cond) && wg_ < (unsigned)kStampWGs)                                                       \
+            g_decode_stamps[(size_t)wg_ * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();    \
+    } while (0)
+#else
+#define PQA_STAMP(slot, cond) \
+    do {                      \
+    } while (0)
+#endif
+
 struct DecodeArgs {
     const float* q;
     const float* k;
@@ -95,7 +126,6 @@ struct DecodeArgs {
 };
 
 constexpr int kDecodeWaves = 8;
-constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kDecodeTiles = 2;  // whole-row workgroups: 16-row K/V tiles in flight per wave
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 16;  // head dims per combine workgroup (HD / 16 workgroups per head)
@@ -111,9 +141,22 @@ constexpr int kShortMaxTiles = 4;  // per-column workgroups: most tiles per wave
 // tile), and each wave's O is complete: no lane-group merge after the loop.
 // NT: 16-row tiles in flight per wave. PF: the loop requests the tiles of its
 // next iteration (without it each wave runs one iteration of NT tiles).
-template <int HD, int G, bool PVM, int NT, bool PF>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs a) {
-    constexpr int NW = kDecodeWaves;
+// XW: a ninth wave that only appends the new row and scores it, so no history
+// wave carries that chain (single-split per-column launches of 4 tiles per
+// wave, where the history waves are long enough for it to pay: C1 7.31 ->
+// 6.97 us; with shorter histories the new-row wave, third on its SIMD, ends
+// later than a history wave doing it would). Raising its issue priority
+// (1 or 2) measured slower: it then delays the two history waves beside it.
+template <bool XW>
+constexpr int decode_threads() {
+    return 64 * (kDecodeWaves + (XW ? 1 : 0));
+}
+
+template <int HD, int G, bool PVM, int NT, bool PF, bool XW>
+__global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const DecodeArgs a) {
+    static_assert(!XW || PVM, "the new-row wave serves per-column workgroups");
+    constexpr int NW = kDecodeWaves;  // history waves
+    constexpr int NT_THREADS = decode_threads<XW>();
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
     constexpr int LPR = HD / 8;       // lanes per V row (8 fp16 each)
     constexpr int VL = 4 * LPR / 16;  // V loads per lane per 16-row tile
@@ -142,13 +185,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int split = blockIdx.x;
     const int ybase = blockIdx.y * a.cpw;
+    PQA_STAMP(kStStart, threadIdx.x == 0);
     const int cols = min(a.ny - ybase, a.cpw);
     const int sub = NW / cols;
     const bool active = w < cols * sub;
     const int c = active ? w % cols : 0;
     const int sb = active ? w / cols : 0;
     const bool owner = split == a.nsplit - 1;
-    const bool writer = active && owner && sb == 0;  // this wave adds column c's new row
+    // the wave that adds column c's new row: the new-row wave, else the
+    // column's first history wave
+    const bool writer = owner && (XW ? w == NW : active && sb == 0);
     // column c = (KV head, chunk of at most G query heads)
     const int kvh = (ybase + c) / a.nchunk;
     const int hc = ybase + c - kvh * a.nchunk;
@@ -216,9 +262,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     pin(wk);
     pin(cs);
     pin(sn);
+    PQA_STAMP(kStIssued + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
 
-    float* q_lds = sq[w];
-    if (active) {
+    float* q_lds = sq[min(w, NW - 1)];
+    if (active || writer) {
         // QK-RMSNorm. q only feeds scores: an fp32 tree sum over the head's
         // H4 lanes. K is stored, so its scale follows the reference's
         // summation order (cpp/tensor.hpp:146-176): quad j sums x[j], x[j+4],
@@ -233,9 +280,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
                                rms_apply(vq[r].z, sc, wq.z), rms_apply(vq[r].w, sc, wq.w)};
             }
             if (writer) {
-                if (lane < H4) ((float4*)skr[w])[t] = vk;
+                float* kr = skr[XW ? 0 : w];
+                if (lane < H4) ((float4*)kr)[t] = vk;
                 wave_sync();
-                const float sc = rms_scale_ref_quad(skr[w], HD, lane & 3);
+                const float sc = rms_scale_ref_quad<HD>(kr, lane & 3);
                 vk = float4{rms_apply(vk.x, sc, wk.x), rms_apply(vk.y, sc, wk.y), rms_apply(vk.z, sc, wk.z),
                             rms_apply(vk.w, sc, wk.w)};
             }
@@ -249,8 +297,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
 #pragma unroll
         for (int r = 0; r < QL; r++) {
             const int i = lane + 64 * r;
-            if (i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
+            if (active && i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
         }
+        PQA_STAMP(kStNewRow0, writer && lane == 0);
         if (writer) {
             // new K/V row: rotate, round to fp16 as the reference does, store
             // once per KV head (chunk 0), keep the rounded values for the merge
@@ -279,6 +328,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
         }
     }
     wave_sync();
+    PQA_STAMP(kStNewRow1, writer && lane == 0);
+    PQA_STAMP(kStQReady + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
 
     // ---------------- wave loop over history rows ----------------
     // Lane (g, n), g = lane/16, n = lane%16. The score MFMA reads K row n of the
@@ -303,6 +354,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
         }
     }
     wave_sync();  // q_lds is reused below for the wave partial
+    PQA_STAMP(kStLoop0 + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
 
     float m_run = NEG_INF;
     float l_run = 0.0f;
@@ -431,6 +483,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
         __builtin_amdgcn_s_setprio(0);
     }
 
+    PQA_STAMP(kStLoop1 + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
     // ---------------- merge the four lane groups, then write the wave partial ----------------
     // Cross-lane sums by DPP / permlane swaps: lane groups differ in lane bits
     // 4 and 5; with HD 64 the two V rows of a lane group differ in bit 3.
@@ -438,7 +491,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
         // m_run is already common to the lane groups and O^T complete: sum l,
         // store lane (g, n)'s O^T[16 m + 4 g + r][n] as head n's dims
         const float l = sum_x32(sum_x16(l_run));
-        if (n < G) {
+        if (n < G && w < NW) {
 #pragma unroll
             for (int m = 0; m < NM; m++) *(floatx4*)(q_lds + n * QS + 16 * m + 4 * grp) = o[m];
             if (grp == 0) {
@@ -475,11 +528,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
     }
     __syncthreads();
 
+    PQA_STAMP(kStMerge, threadIdx.x == 0);
     // ---------------- workgroup merge per column (+ the new row) ----------------
     // one float4 of head dims per thread and item
     const int tid = threadIdx.x;
     constexpr int D4 = HD / 4;
-    for (int i = tid; i < cols * G * D4; i += kDecodeThreads) {
+    for (int i = tid; i < cols * G * D4; i += NT_THREADS) {
         const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
         const int yk = (ybase + cc) / a.nchunk;
         const int yc = ybase + cc - yk * a.nchunk;
@@ -508,6 +562,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeArgs
             if (d4 == 0) *(float2*)(a.part_ml + pb * 2) = float2{M, L};
         }
     }
+#ifdef PQA_PHASE_STAMPS
+    __syncthreads();  // the stamped build only: every output stored before the end stamp
+#endif
+    PQA_STAMP(kStEnd, threadIdx.x == 0);
 }
 
 // Merge of the split partials of one column: workgroup (head h, column y,
@@ -680,11 +738,13 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
 // heads per column made the VALU PV the bound there), with 1, 2 or 4 tiles per
 // wave (4: two in flight, two iterations); whole-row workgroups stream HBM and
 // keep the VALU PV.
-template <int HD, bool PVM, int NT, bool PF>
+template <int HD, bool PVM, int NT, bool PF, bool XW = false>
 static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
     switch (G) {
 #define PQA_CASE(GG) \
-    case GG: hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF>), grid, dim3(kDecodeThreads), 0, st, a); break;
+    case GG:                                                                                                   \
+        hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF, XW>), grid, dim3(decode_threads<XW>()), 0, st, a); \
+        break;
         PQA_CASE(1) PQA_CASE(2) PQA_CASE(3) PQA_CASE(4) PQA_CASE(5) PQA_CASE(6) PQA_CASE(7) PQA_CASE(8)
 #undef PQA_CASE
         default: return hipErrorInvalidValue;
@@ -698,7 +758,7 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 g
     if (a.cpw != 1) le = launch_decode_pv<HD, false, kDecodeTiles, true>(a, G, grid, st);
     else if (tiles == 1) le = launch_decode_pv<HD, true, 1, false>(a, G, grid, st);
     else if (tiles == 2) le = launch_decode_pv<HD, true, 2, false>(a, G, grid, st);
-    else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true>(a, G, grid, st);
+    else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true, true>(a, G, grid, st);  // one split
     if (le != hipSuccess) return le;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
@@ -708,6 +768,23 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 g
                        a.part_ml, a.out, G, a.g, a.nchunk, a.nsplit);
     return hipGetLastError();
 }
+
+#ifdef PQA_PHASE_STAMPS
+// The stamped build's extra entry points (not in pqa.h): copy out / clear the
+// stamps of the last decode launches; n = kStampWGs * kStampSlots values.
+extern "C" int pqa_decode_stamps_read(unsigned long long* dst, int n) {
+    if (!dst || n != kStampWGs * kStampSlots) return PQA_ERR_ARG;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_stamps), (size_t)n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess
+               ? PQA_OK
+               : PQA_ERR_HIP;
+}
+extern "C" int pqa_decode_stamps_clear() {
+    static unsigned long long zero[kStampWGs * kStampSlots];
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_decode_stamps), zero, sizeof(zero), 0, hipMemcpyHostToDevice) == hipSuccess
+               ? PQA_OK
+               : PQA_ERR_HIP;
+}
+#endif
 
 hipError_t launch_decode(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k,
                          const float* v, float* out, const DecodeWorkspace& ws) {

@@ -76,12 +76,35 @@ __device__ __forceinline__ float rms_scale_ref_quad(const float* x, int n, int j
 #pragma clang fp contract(off)
     float l = 0.0f;
     const int nfull = n & ~3;
+    // the reads do not depend on the sums: unrolled, they are all in flight
+    // before the (sequential) adds need them
+#pragma unroll 8
     for (int i = j; i < nfull; i += 4) l = l + x[i] * x[i];
     const float L0 = __shfl(l, 0, 4), L1 = __shfl(l, 1, 4);
     const float L2 = __shfl(l, 2, 4), L3 = __shfl(l, 3, 4);
     float ss = (L0 + L2) + (L1 + L3);
     for (int i = nfull; i < n; i++) ss = ss + x[i] * x[i];
     return 1.0f / sqrtf(ss / (float)n + 1e-6f);
+}
+
+// The same for a head size known at compile time (N a multiple of 4): a fixed
+// trip count, so all N / 4 reads of lane j are issued before the adds, which
+// keep their order (a loop with the lane-dependent bound above read one value
+// per LDS round trip: 1.8 us at N = 128).
+template <int N>
+__device__ __forceinline__ float rms_scale_ref_quad(const float* x, int j) {
+#pragma clang fp contract(off)
+    static_assert(N % 4 == 0, "whole SSE groups");
+    float v[N / 4];
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) v[k] = x[4 * k + j];
+    float l = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) l = l + v[k] * v[k];
+    const float L0 = __shfl(l, 0, 4), L1 = __shfl(l, 1, 4);
+    const float L2 = __shfl(l, 2, 4), L3 = __shfl(l, 3, 4);
+    const float ss = (L0 + L2) + (L1 + L3);
+    return 1.0f / sqrtf(ss / (float)N + 1e-6f);
 }
 
 // Element indices of RoPE pair p (0 <= p < hd/2) for each pairing; the angle

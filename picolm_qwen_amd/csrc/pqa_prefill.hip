@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) 
         ((float4*)sk[w][hh])[t] = kx;
         wave_sync();
         const int qd = min(lane >> 2, IPW - 1);  // quad qd sums row qd in the reference's order
-        const float s = rms_scale_ref_quad(sk[w][qd], HD, lane & 3);
+        const float s = rms_scale_ref_quad<HD>(sk[w][qd], lane & 3);
         if ((lane & 3) == 0 && (lane >> 2) < IPW) s_scale[w][qd] = s;
         wave_sync();
         const float sc = s_scale[w][hh];
