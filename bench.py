@@ -837,6 +837,60 @@ STAMP_PHASES = [("prologue loads issued", 1), ("q ready (norm, RoPE, LDS)", 10),
 STAMP_MERGE, STAMP_END, STAMP_NEW0, STAMP_NEW1 = 37, 38, 39, 40
 
 
+PSTAMP_SLOTS, PSTAMP_WGS = 64, 4096
+
+
+def prefill_phase_stamps(reps=5):
+    """Per-phase timings of the prefill attention kernel from the stamped build:
+    the Qwen3-4B prefill of 2048 tokens (one layer, QK-norm, default hi + lo q).
+    Per row block (each workgroup runs a long block, then a short one), the
+    median over reps launches of the per-workgroup means (µs from the
+    workgroup's first stamp)."""
+    import torch
+    from picolm_qwen_amd import _lib
+    L = _lib.stamped_lib()
+    dev = torch.device("cuda:0")
+    nh, nkv, hd, s = 32, 8, 128, 2048
+    cx = Ctx(1, s, nh, nkv, hd, 0, 1e6, L=L)
+    rng = np.random.default_rng(4242)
+    set_norms(cx, rng, hd)
+    q, k, v, out = make_inputs(torch, dev, rng, 1, s, nh, nkv, hd)
+    torch.cuda.synchronize()
+    args = [C.c_void_p(t[0].data_ptr()) for t in (q, k, v, out)]
+    _, ev = timed(torch, cx, lambda: L.pqa_prefill(cx.h, 0, 0, s, *args), 10, 3)
+    rows = []
+    for _ in range(reps):
+        cx.check(L.pqa_prefill_stamps_clear())
+        cx.check(L.pqa_prefill(cx.h, 0, 0, s, *args), cx.h)
+        cx.check(L.pqa_sync(cx.h), cx.h)
+        a = np.zeros(PSTAMP_WGS * PSTAMP_SLOTS, np.uint64)
+        cx.check(L.pqa_prefill_stamps_read(a.ctypes.data_as(C.c_void_p), a.size))
+        a = a.reshape(PSTAMP_WGS, PSTAMP_SLOTS).astype(np.int64)
+        a = a[a[:, 0] > 0]
+        t0 = a[:, :1]
+        rel = np.where(a > 0, (a - t0) / 100.0, np.nan)
+        ends = np.nanmax(np.where(a > 0, a, np.nan), 1)
+        rows.append((len(a), rel, (np.nanmax(ends) - a[:, 0].min()) / 100.0,
+                     (a[:, 0].max() - a[:, 0].min()) / 100.0))
+    med = np.nanmedian(np.stack([np.nanmean(r, 0) for _, r, _, _ in rows]), 0)
+    span = float(np.median([x[2] for x in rows]))
+    spread = float(np.median([x[3] for x in rows]))
+    lines = [f"prefill 2048 tokens, 32/8 heads, hd 128, QK-norm, hi + lo q: {rows[0][0]} workgroups; "
+             f"{ev * 1e3:.1f} us per call event-timed (stamped build, with the K/V prep launch); "
+             f"first start to last stamp {span:.1f} us; workgroup starts spread over {spread:.2f} us",
+             f"  us from the workgroup's start (mean over workgroups, median of {reps} launches); "
+             "waves 0-3 take even key tiles, 4-7 odd ones"]
+    for j, name in ((0, "long block"), (1, "short block")):
+        b = 32 * j
+        lines.append(f"  {name}: starts {med[b]:6.2f}")
+        lines.append("    q ready         " + " ".join(f"{x:6.2f}" for x in med[b + 1:b + 9]))
+        lines.append("    tile loop done  " + " ".join(f"{x:6.2f}" for x in med[b + 9:b + 17]))
+        lines.append(f"    partials merged {med[b + 17]:6.2f}")
+        lines.append("    rows stored     " + " ".join(f"{x:6.2f}" for x in med[b + 18:b + 22]))
+    cx.close()
+    return "\n".join(lines)
+
+
 def phase_stamps(cases=None, reps=7):
     """Per-phase timings of single decode launches from the stamped build: for
     each case, the median over reps launches of each wave's stamps relative to
@@ -908,10 +962,11 @@ def main():
                     help="per-dispatch counter averages of the kernels named by --kernel")
     ap.add_argument("--kernel", default="prefill_attn_kernel")
     ap.add_argument("--phase-stamps", action="store_true",
-                    help="per-phase decode timings from the stamped build (libpqa_stamps.so)")
+                    help="per-phase decode and prefill timings from the stamped build (libpqa_stamps.so)")
     args = ap.parse_args()
     if args.phase_stamps:
         print(phase_stamps(), flush=True)
+        print(prefill_phase_stamps(), flush=True)
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.kernel))

@@ -50,8 +50,8 @@ def lib() -> C.CDLL:
 
 def stamped_lib() -> C.CDLL:
     """The phase-stamped build of the same sources (measurement only: its
-    kernels also write s_memrealtime stamps; pqa_decode_stamps_read and
-    pqa_decode_stamps_clear return them)."""
+    kernels also write s_memrealtime stamps; pqa_decode_stamps_read /
+    pqa_prefill_stamps_read return them, the _clear calls zero them)."""
     global _stamped
     if _stamped is None:
         if not os.path.exists(STAMPS_LIB):
@@ -61,6 +61,10 @@ def stamped_lib() -> C.CDLL:
         L.pqa_decode_stamps_read.restype = C.c_int
         L.pqa_decode_stamps_clear.argtypes = []
         L.pqa_decode_stamps_clear.restype = C.c_int
+        L.pqa_prefill_stamps_read.argtypes = [C.c_void_p, C.c_int]
+        L.pqa_prefill_stamps_read.restype = C.c_int
+        L.pqa_prefill_stamps_clear.argtypes = []
+        L.pqa_prefill_stamps_clear.restype = C.c_int
         _stamped = L
     return _stamped
 

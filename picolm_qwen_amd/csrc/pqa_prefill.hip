@@ -117,6 +117,33 @@ __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) 
     }
 }
 
+// Phase stamps of prefill_attn_kernel, compiled in only with
+// -DPQA_PHASE_STAMPS (bench.py --phase-stamps): s_memrealtime (100 MHz) per
+// wave at the phase boundaries of each of the workgroup's two row blocks,
+// kPStampSlots per workgroup (block j at 32 j), read back by
+// pqa_prefill_stamps_read.
+constexpr int kPStampSlots = 64;
+constexpr int kPStampWGs = 4096;
+enum : int {
+    kPStStart = 0,   // block start (thread 0)
+    kPStQReady = 1,  // + wave: q normed, rotated, fp16 in LDS
+    kPStLoop = 9,    // + wave: tile loop done
+    kPStMerged = 17, // odd-tile partials merged (thread 0)
+    kPStStored = 18, // + wave (even-tile waves): output rows stored
+};
+#ifdef PQA_PHASE_STAMPS
+static __device__ unsigned long long g_prefill_stamps[kPStampWGs * kPStampSlots];
+#define PQA_PSTAMP(slot, cond)                                                                           \
+    do {                                                                                                 \
+        if ((cond) && blockIdx.x < (unsigned)kPStampWGs)                                                 \
+            g_prefill_stamps[(size_t)blockIdx.x * kPStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define PQA_PSTAMP(slot, cond) \
+    do {                       \
+    } while (0)
+#endif
+
 struct AttnArgs {
     const float* q;   // fp32 projections: row of token t at q + t * q_ld, heads one after the other
     const float* qn;  // [HD] or null
@@ -197,6 +224,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
     for (int j = 0; j < nb; j++) {
         const int b = j == 0 ? a.nblk - 1 - pair : pair;
         if (j) __syncthreads();  // the previous block's epilogue is done with the LDS
+        PQA_PSTAMP(32 * j + kPStStart, tid == 0);
 
         // Lane-derived offsets are rebuilt for each block (the empty asm hides
         // that the lane id is loop-invariant), so they are not held live, and
@@ -430,6 +458,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         }
         const char* sq_row = sq[wr] + col * HD * 2;
         auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
+        PQA_PSTAMP(32 * j + kPStQReady + w, (tid & 63) == 0);
 
         // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
         // a row whose keys in a tile are all masked (the odd group's first tile
@@ -563,6 +592,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             if (step + 1 < nsteps) tile(step + 1, std::integral_constant<int, 1>{});
         }
 
+        PQA_PSTAMP(32 * j + kPStLoop + w, (tid & 63) == 0);
         // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
         // LDS: [wr][MR][64 lanes] floats: o (16 DT per lane), m, l.
         constexpr int MR = 16 * DT + 2;
@@ -578,6 +608,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             mg[(MR - 1) * 64 + lane] = l_run;
         }
         __syncthreads();
+        PQA_PSTAMP(32 * j + kPStMerged, tid == 0);
         if (par == 0) {
             {
                 const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
@@ -624,9 +655,28 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 const floatx4 vv = *(const floatx4*)(mg + rr * HD + 4 * (c ^ (rr & (CPR - 1))));
                 if (orr >= 0) *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv;
             }
+            PQA_PSTAMP(32 * j + kPStStored + w, lane == 0);
         }
     }
 }
+
+#ifdef PQA_PHASE_STAMPS
+// The stamped build's extra entry points (not in pqa.h), as for decode.
+extern "C" int pqa_prefill_stamps_read(unsigned long long* dst, int n) {
+    if (!dst || n != kPStampWGs * kPStampSlots) return PQA_ERR_ARG;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_prefill_stamps), (size_t)n * 8, 0, hipMemcpyDeviceToHost) ==
+                   hipSuccess
+               ? PQA_OK
+               : PQA_ERR_HIP;
+}
+extern "C" int pqa_prefill_stamps_clear() {
+    static unsigned long long zero[kPStampWGs * kPStampSlots];
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_prefill_stamps), zero, sizeof(zero), 0, hipMemcpyHostToDevice) ==
+                   hipSuccess
+               ? PQA_OK
+               : PQA_ERR_HIP;
+}
+#endif
 
 template <int HD, bool YS>
 static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_tok, const float* q,
