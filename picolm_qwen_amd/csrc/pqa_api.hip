@@ -172,7 +172,9 @@ extern "C" int pqa_decode(pqa_ctx* ctx, int layer, int pos, const float* q, cons
     if (int rc = check_layer(ctx, layer, "pqa_decode")) return rc;
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: NULL buffer");
-    if (misaligned(ctx, q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_decode: buffers must be 16-byte aligned");
+    if (misaligned(ctx, q, k, v, out))
+        return set_err(ctx, PQA_ERR_ARG,
+                       "pqa_decode: misaligned buffer (16 bytes for head_dim 64/128; else q/k/v 4, out 8)");
     const pqa::DecodeWorkspace ws{ctx->part_acc, ctx->part_ml, ctx->max_splits};
     return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out, ws), "pqa_decode");
 }
@@ -188,7 +190,8 @@ extern "C" int pqa_decode_noalloc(pqa_ctx* ctx, int layer, int pos, const float*
     if (pos < 0 || pos >= ctx->max_seq_len) return set_err(ctx, PQA_ERR_RANGE, "pqa_decode_noalloc: pos out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: NULL buffer");
     if (misaligned(ctx, q, k, v, out))
-        return set_err(ctx, PQA_ERR_ARG, "pqa_decode_noalloc: buffers must be 16-byte aligned");
+        return set_err(ctx, PQA_ERR_ARG,
+                       "pqa_decode_noalloc: misaligned buffer (16 bytes for head_dim 64/128; else q/k/v 4, out 8)");
     pqa::DecodeWorkspace ws;
     if (int rc = pqa::scratch_workspace(ctx, &ws, fn)) return rc;
     return hip_check(ctx, pqa::launch_decode(ctx, layer, pos, q, k, v, out, ws), fn);
@@ -202,7 +205,9 @@ extern "C" int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, co
     if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill: positions out of range");
     if (!q || !k || !v || !out) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: NULL buffer");
-    if (misaligned(ctx, q, k, v, out)) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill: buffers must be 16-byte aligned");
+    if (misaligned(ctx, q, k, v, out))
+        return set_err(ctx, PQA_ERR_ARG,
+                       "pqa_prefill: misaligned buffer (16 bytes for head_dim 64/128; else q/k/v 4, out 8)");
     return hip_check(ctx, pqa::launch_prefill(ctx, layer, start_pos, n_tok, q, k, v, out), "pqa_prefill");
 }
 

@@ -123,58 +123,32 @@ struct GenAttnArgs {
     int start, n_tok, nh, hd, kv_dim, g, nchunk, G, ny, rps, nsplit;
 };
 
-// Keys of a tile: lane j takes key k0 + j and walks its K row in VW-half
-// steps (VW = 8: 16-byte loads, head_dim a multiple of 8; VW = 2 otherwise).
-template <int VW, int QW>
-__device__ __forceinline__ void gen_scores(const uint16_t* krow, const float (*q)[QW], int hd, int Gc,
-                                           float (&sc)[kGenMaxG]) {
+// Keys of a tile (head_dim not a multiple of 8): lane j takes key k0 + j and
+// walks its K row in fp16 pairs.
+template <int QW>
+__device__ __forceinline__ void gen_scores2(const uint16_t* krow, const float (*q)[QW], int hd, int Gc,
+                                            float (&sc)[kGenMaxG]) {
 #pragma unroll
     for (int h = 0; h < kGenMaxG; h++) sc[h] = 0.0f;
-    if constexpr (VW == 8) {
-        const u32x4* kr = (const u32x4*)krow;
-#pragma unroll 2
-        for (int d8 = 0; d8 < hd / 8; d8++) {
-            const u32x4 u = kr[d8];
-            float kf[8];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                kf[2 * e] = f16_bits_to_f32((uint16_t)(u[e] & 0xFFFFu));
-                kf[2 * e + 1] = f16_bits_to_f32((uint16_t)(u[e] >> 16));
-            }
-#pragma unroll
-            for (int h = 0; h < kGenMaxG; h++) {
-                if (h < Gc) {
-                    const floatx4 q0 = *(const floatx4*)&q[h][8 * d8];
-                    const floatx4 q1 = *(const floatx4*)&q[h][8 * d8 + 4];
-                    float s = sc[h];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) s = fmaf(q0[e], kf[e], s);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) s = fmaf(q1[e], kf[4 + e], s);
-                    sc[h] = s;
-                }
-            }
-        }
-    } else {
-        const uint32_t* kr = (const uint32_t*)krow;
+    const uint32_t* kr = (const uint32_t*)krow;
 #pragma unroll 4
-        for (int d2 = 0; d2 < hd / 2; d2++) {
-            const uint32_t u = kr[d2];
-            const float k0 = f16_bits_to_f32((uint16_t)(u & 0xFFFFu)), k1 = f16_bits_to_f32((uint16_t)(u >> 16));
+    for (int d2 = 0; d2 < hd / 2; d2++) {
+        const uint32_t u = kr[d2];
+        const float k0 = f16_bits_to_f32((uint16_t)(u & 0xFFFFu)), k1 = f16_bits_to_f32((uint16_t)(u >> 16));
 #pragma unroll
-            for (int h = 0; h < kGenMaxG; h++) {
-                if (h < Gc) {
-                    const float2 qq = *(const float2*)&q[h][2 * d2];
-                    sc[h] = fmaf(qq.y, k1, fmaf(qq.x, k0, sc[h]));
-                }
+        for (int h = 0; h < kGenMaxG; h++) {
+            if (h < Gc) {
+                const float2 qq = *(const float2*)&q[h][2 * d2];
+                sc[h] = fmaf(qq.y, k1, fmaf(qq.x, k0, sc[h]));
             }
         }
     }
 }
 
-// NS: fp16 pairs per lane in the PV product (hd / 2 <= 64 NS); the q rows in
-// LDS are 128 NS floats wide (18 KB per workgroup for NS = 1).
-template <int NS, int VW>
+// Head sizes that are not a multiple of 8 (4-byte loads). NS: fp16 pairs per
+// lane in the PV product (hd / 2 <= 64 NS); the q rows in LDS are 128 NS
+// floats wide (24 KB per workgroup for NS = 1).
+template <int NS>
 __global__ __launch_bounds__(64 * kGenWaves) void gen_attn_kernel(const GenAttnArgs a) {
     constexpr int QW = 128 * NS;
     __shared__ __attribute__((aligned(16))) float s_q[kGenWaves][kGenMaxG][QW];
@@ -216,7 +190,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void gen_attn_kernel(const GenAttnA
         const int key = k0 + lane;
         const bool valid = key < kend;
         float sc[kGenMaxG];
-        gen_scores<VW, QW>(kbase + (size_t)(valid ? key : kbeg) * a.kv_dim, q, hd, Gc, sc);
+        gen_scores2<QW>(kbase + (size_t)(valid ? key : kbeg) * a.kv_dim, q, hd, Gc, sc);
 #pragma unroll
         for (int h = 0; h < kGenMaxG; h++) {
             if (h < Gc) {
@@ -530,7 +504,7 @@ static hipError_t launch_gen_prep(pqa_ctx* ctx, int layer, int start, int n_tok,
 
 template <int NS>
 static hipError_t launch_gen_attn_ns(const GenAttnArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((gen_attn_kernel<NS, 2>), grid, dim3(64 * kGenWaves), 0, st, a);
+    hipLaunchKernelGGL((gen_attn_kernel<NS>), grid, dim3(64 * kGenWaves), 0, st, a);
     return hipGetLastError();
 }
 
