@@ -902,7 +902,9 @@ def phase_stamps(cases=None, reps=7):
     cases = cases or [("tinyllama ctx 512 (32/4 heads, hd 64, block8)", 32, 4, 64, 1, 1e4, 511, False),
                       ("qwen2.5-0.5b ctx 1 (14/2 heads, hd 64)", 14, 2, 64, 0, 1e6, 0, False),
                       ("qwen2.5-0.5b ctx 301 (14/2 heads, hd 64)", 14, 2, 64, 0, 1e6, 300, False),
-                      ("qwen3 16/8 heads hd 128, ctx 201, QK-norm", 16, 8, 128, 0, 1e6, 200, True)]
+                      ("qwen3 16/8 heads hd 128, ctx 201, QK-norm", 16, 8, 128, 0, 1e6, 200, True),
+                      ("qwen3-1.7b ctx 32768 (16/8 heads, hd 128, QK-norm; whole-row workgroups)",
+                       16, 8, 128, 0, 1e6, 32767, True)]
     lines = []
     for name, nh, nkv, hd, style, base, pos, qk in cases:
         cx = Ctx(1, pos + 1, nh, nkv, hd, style, base, L=L)
@@ -925,12 +927,18 @@ def phase_stamps(cases=None, reps=7):
             a = a.reshape(STAMP_WGS, STAMP_SLOTS).astype(np.int64)
             a = a[a[:, 0] > 0]
             rel = np.where(a > 0, (a - a[:, :1]) / 100.0, np.nan)
-            per.append((len(a), rel, (a[:, STAMP_END].max() - a[:, 0].min()) / 100.0))
+            per.append((len(a), rel, (a[:, STAMP_END].max() - a[:, 0].min()) / 100.0,
+                        (a[:, 0] - a[:, 0].min()) / 100.0, (a[:, STAMP_END] - a[:, 0].min()) / 100.0))
         nwg = per[0][0]
-        med = np.nanmedian(np.stack([np.nanmean(r, 0) for _, r, _ in per]), 0)
-        span = float(np.median([sp for _, _, sp in per]))
+        med = np.nanmedian(np.stack([np.nanmean(x[1], 0) for x in per]), 0)
+        span = float(np.median([x[2] for x in per]))
         lines.append(f"{name}: {nwg} workgroup(s); {ev * 1e3:.2f} us per call event-timed (stamped build); "
                      f"first start to last end {span:.2f} us")
+        if nwg > 8:
+            st = np.median(np.stack([np.percentile(x[3], [0, 50, 100]) for x in per]), 0)
+            en = np.median(np.stack([np.percentile(x[4], [0, 50, 100]) for x in per]), 0)
+            lines.append(f"  workgroup starts (min/median/max, us after the first) {st[0]:.2f} / {st[1]:.2f} / "
+                         f"{st[2]:.2f}; ends {en[0]:.2f} / {en[1]:.2f} / {en[2]:.2f}")
         lines.append("  us from the workgroup's start, per wave 0..8 (mean over workgroups, median of "
                      f"{reps} launches; '  -  ': the wave has no such phase)")
         for label, off in STAMP_PHASES:
