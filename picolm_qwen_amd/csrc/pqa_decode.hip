@@ -252,6 +252,18 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const int ci = rope_angle_f4<HD>(a.rope, t);
     float4 cs = ((const float4*)a.cosr)[ci];
     float4 sn = ((const float4*)a.sinr)[ci];
+    // Per-column workgroups with history: every wave's small loads enter the
+    // memory pipe before any wave's tiles; otherwise the older wave of each
+    // SIMD queues its tiles ahead of the younger one's q, and the younger wave
+    // starts its loop a round trip late (an execution barrier only; nothing
+    // waits for the loads). C1 7.03 -> 6.82 us, Qwen2.5-0.5B sweep 8.13 ->
+    // 7.80 us. Whole-row workgroups keep the old order: with it C3 measured
+    // +0.35 us (their older waves lose more by the later start of their tiles
+    // than the younger ones gain) and C5 +0.3 us even with the barrier
+    // skipped at run time.
+    if constexpr (PVM) {
+        if (r1 > r0) __builtin_amdgcn_s_barrier();  // the same for every wave of the workgroup
+    }
 #pragma unroll
     for (int b = 0; b < NT; b++) load_tile(w0 + 16 * b, kt[b], vt[b]);
 #pragma unroll
