@@ -883,6 +883,8 @@ def prefill_phase_stamps(reps=5):
     for j, name in ((0, "long block"), (1, "short block")):
         b = 32 * j
         lines.append(f"  {name}: starts {med[b]:6.2f}")
+        lines.append(f"    q rows landed {med[b + 22]:6.2f}   (wave 0: q and the first tiles in LDS)")
+        lines.append(f"    q math done   {med[b + 23]:6.2f}   (wave 0: normed, rotated, fp16 in LDS)")
         lines.append("    q ready         " + " ".join(f"{x:6.2f}" for x in med[b + 1:b + 9]))
         lines.append("    tile loop done  " + " ".join(f"{x:6.2f}" for x in med[b + 9:b + 17]))
         lines.append(f"    partials merged {med[b + 17]:6.2f}")

@@ -130,6 +130,8 @@ enum : int {
     kPStLoop = 9,    // + wave: tile loop done
     kPStMerged = 17, // odd-tile partials merged (thread 0)
     kPStStored = 18, // + wave (even-tile waves): output rows stored
+    kPStQLanded = 22,  // wave 0: raw q rows (and the first tiles) landed in LDS
+    kPStQMath = 23,    // wave 0: q normed, rotated and written as fp16
 };
 #ifdef PQA_PHASE_STAMPS
 static __device__ unsigned long long g_prefill_stamps[kPStampWGs * kPStampSlots];
@@ -372,6 +374,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();  // q rows and s_qw landed
+            PQA_PSTAMP(32 * j + kPStQLanded, tid == 0);
             float x[NF][4];
             const char* rowp = qst + prow * HD * 4;
 #pragma unroll
@@ -448,6 +451,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 *(half8*)(sq[wr] + prow * HD * 2 + slot) = hi8;
                 if constexpr (SPLITQ) *(half8*)(qst + prow * HD * 4 + slot) = lo8;
             }
+            PQA_PSTAMP(32 * j + kPStQMath, tid == 0);
             if constexpr (SPLITQ) {
                 __syncthreads();  // both waves' residual rows landed
                 const char* lrow = qst + col * HD * 4;
