@@ -542,21 +542,18 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
 
     PQA_STAMP(kStMerge, threadIdx.x == 0);
     // ---------------- workgroup merge per column (+ the new row) ----------------
-    // one float4 of head dims per thread and item
+    // One float4 of head dims per thread and item: column cc (KV head yk,
+    // chunk yc), head h; the column's nsub wave partials sit at waves
+    // cc, cc + wstride, ...
     const int tid = threadIdx.x;
     constexpr int D4 = HD / 4;
-    for (int i = tid; i < cols * G * D4; i += NT_THREADS) {
-        const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
-        const int yk = (ybase + cc) / a.nchunk;
-        const int yc = ybase + cc - yk * a.nchunk;
-        const int gq = min(G, a.g - yc * G);
-        if (h >= gq) continue;
+    auto merge = [&](int cc, int h, int d4, int yk, int yc, int nsub, int wstride) {
         float M = owner ? s_new[cc][h] : NEG_INF;
-        for (int s = 0; s < sub; s++) M = fmaxf(M, wm[cc + s * cols][h]);
+        for (int s = 0; s < nsub; s++) M = fmaxf(M, wm[cc + s * wstride][h]);
         float L = 0.0f;
         floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s = 0; s < sub; s++) {
-            const int wv = cc + s * cols;
+        for (int s = 0; s < nsub; s++) {
+            const int wv = cc + s * wstride;
             const float e = fast_exp2(wm[wv][h] - M);
             L += e * wl[wv][h];
             A += e * *(const floatx4*)&sq[wv][h * QS + 4 * d4];
@@ -567,11 +564,26 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
             A += e * *(const floatx4*)&s_vnew[cc][4 * d4];
         }
         if (a.nsplit == 1) {
-            ((floatx4*)(a.out + (size_t)(yk * a.g + yc * G + h) * HD))[d4] = A / L;
+            ((floatx4*)(a.out + (size_t)(yk * a.g + yc * G + h) * HD))[d4] = A * (1.0f / L);
         } else {
             const size_t pb = ((size_t)(ybase + cc) * a.nsplit + split) * G + h;
             ((floatx4*)(a.part_acc + pb * HD))[d4] = A;
             if (d4 == 0) *(float2*)(a.part_ml + pb * 2) = float2{M, L};
+        }
+    };
+    if constexpr (PVM) {
+        // Per-column workgroups: one column, its NW history waves in order,
+        // counts known at compile time, so every LDS read of an item is
+        // issued before the first is used; at most 256 items, one per thread.
+        static_assert(G * D4 <= NT_THREADS, "one merge item per thread");
+        if (tid < Gc * D4) merge(0, tid / D4, tid % D4, kvh, hc, NW, 1);
+    } else {
+        for (int i = tid; i < cols * G * D4; i += NT_THREADS) {
+            const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
+            const int yk = (ybase + cc) / a.nchunk;
+            const int yc = ybase + cc - yk * a.nchunk;
+            if (h >= min(G, a.g - yc * G)) continue;
+            merge(cc, h, d4, yk, yc, sub, cols);
         }
     }
 #ifdef PQA_PHASE_STAMPS
