@@ -39,6 +39,7 @@
 #include <algorithm>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "pqa_device.h"
 #include "pqa_internal.h"
@@ -578,13 +579,23 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
         static_assert(G * D4 <= NT_THREADS, "one merge item per thread");
         if (tid < Gc * D4) merge(0, tid / D4, tid % D4, kvh, hc, NW, 1);
     } else {
-        for (int i = tid; i < cols * G * D4; i += NT_THREADS) {
-            const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
-            const int yk = (ybase + cc) / a.nchunk;
-            const int yc = ybase + cc - yk * a.nchunk;
-            if (h >= min(G, a.g - yc * G)) continue;
-            merge(cc, h, d4, yk, yc, sub, cols);
-        }
+        // Whole-row workgroups: the usual 8 or 4 columns (1 or 2 waves each)
+        // get compile-time counts too; any other count takes the general loop.
+        auto items = [&](auto ncol) {
+            constexpr int NC = decltype(ncol)::value;
+            const int nc = NC ? NC : cols;
+            const int ns = NC ? NW / NC : sub;
+            for (int i = tid; i < nc * G * D4; i += NT_THREADS) {
+                const int cc = i / (G * D4), h = (i / D4) - cc * G, d4 = i - (i / D4) * D4;
+                const int yk = a.nchunk == 1 ? ybase + cc : (ybase + cc) / a.nchunk;
+                const int yc = ybase + cc - yk * a.nchunk;
+                if (h >= min(G, a.g - yc * G)) continue;
+                merge(cc, h, d4, yk, yc, ns, nc);
+            }
+        };
+        if (cols == 8) items(std::integral_constant<int, 8>{});
+        else if (cols == 4) items(std::integral_constant<int, 4>{});
+        else items(std::integral_constant<int, 0>{});
     }
 #ifdef PQA_PHASE_STAMPS
     __syncthreads();  // the stamped build only: every output stored before the end stamp

@@ -134,6 +134,14 @@ __device__ __forceinline__ void rope_rotate(float& x0, float& x1, float c, float
     x1 = a * s + b * c;
 }
 
+// The same rotation with fused multiply-adds, for values that are not stored
+// (q): two instructions per element instead of three.
+__device__ __forceinline__ void rope_rotate_fma(float& x0, float& x1, float c, float s) {
+    const float a = x0, b = x1;
+    x0 = fmaf(a, c, -(b * s));
+    x1 = fmaf(a, s, b * c);
+}
+
 // (x * s) * w, rounded twice (cpp/tensor.hpp:168-171).
 __device__ __forceinline__ float rms_apply(float x, float s, float w) {
 #pragma clang fp contract(off)

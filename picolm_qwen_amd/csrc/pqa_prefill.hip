@@ -397,6 +397,9 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                     }
                 }
             }
+            // the score scale (log2 e / sqrt(hd), 0 for padding rows) goes in
+            // with the norm scale, or alone without a norm: q is not stored
+            const float qs = pR < a.rows ? a.qscale : 0.0f;
             if (a.qn) {
                 float ss = 0.0f;
 #pragma unroll
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
 #pragma unroll
                     for (int e = 0; e < 4; e++) ss = fmaf(x[i][e], x[i][e], ss);
                 ss = group_sum<4>(ss);  // the row's four lanes
-                const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+                const float sc = qs / sqrtf(ss / (float)HD + 1e-6f);
 #pragma unroll
                 for (int i = 0; i < NF; i++) {
                     const float4 wv = *(const float4*)(s_qw + 4 * pchunk(i));
@@ -413,6 +416,11 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                     x[i][2] = rms_apply(x[i][2], sc, wv.z);
                     x[i][3] = rms_apply(x[i][3], sc, wv.w);
                 }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NF; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) x[i][e] *= qs;
             }
 #pragma unroll
             for (int q = 0; q < NH4; q++) {
@@ -420,21 +428,20 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 const float sv[4] = {sf[q].x, sf[q].y, sf[q].z, sf[q].w};
                 if (a.rope == 0) {  // NeoX: float4 q of half 0 with float4 q of half 1
 #pragma unroll
-                    for (int e = 0; e < 4; e++) rope_rotate(x[q][e], x[NH4 + q][e], cv[e], sv[e]);
+                    for (int e = 0; e < 4; e++) rope_rotate_fma(x[q][e], x[NH4 + q][e], cv[e], sv[e]);
                 } else {
                     const int i0 = (q / (NH4 / 2)) * NH4 + 2 * (q % (NH4 / 2));  // chunk pair (i0, i0 + 1)
                     if (a.rope == 1) {  // block8: element e of the two halves of the 8-dim chunk
 #pragma unroll
-                        for (int e = 0; e < 4; e++) rope_rotate(x[i0][e], x[i0 + 1][e], cv[e], sv[e]);
+                        for (int e = 0; e < 4; e++) rope_rotate_fma(x[i0][e], x[i0 + 1][e], cv[e], sv[e]);
                     } else {  // interleaved: (2i, 2i+1), angles 2c .. 2c+3 over the chunk pair
-                        rope_rotate(x[i0][0], x[i0][1], cv[0], sv[0]);
-                        rope_rotate(x[i0][2], x[i0][3], cv[1], sv[1]);
-                        rope_rotate(x[i0 + 1][0], x[i0 + 1][1], cv[2], sv[2]);
-                        rope_rotate(x[i0 + 1][2], x[i0 + 1][3], cv[3], sv[3]);
+                        rope_rotate_fma(x[i0][0], x[i0][1], cv[0], sv[0]);
+                        rope_rotate_fma(x[i0][2], x[i0][3], cv[1], sv[1]);
+                        rope_rotate_fma(x[i0 + 1][0], x[i0 + 1][1], cv[2], sv[2]);
+                        rope_rotate_fma(x[i0 + 1][2], x[i0 + 1][3], cv[3], sv[3]);
                     }
                 }
             }
-            const float qs = pR < a.rows ? a.qscale : 0.0f;
             __syncthreads();  // every wave is done with the norm weights in sq
             // fp16 chunk (i0 / 2) = float4s (i0, i0 + 1); hi to sq, the residual
             // (split-q) over the row's own fp32 staging
@@ -443,7 +450,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 half8 hi8, lo8;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const float xs = x[i0 + e / 4][e % 4] * qs;
+                    const float xs = x[i0 + e / 4][e % 4];
                     hi8[e] = (_Float16)xs;
                     lo8[e] = (_Float16)(xs - (float)hi8[e]);
                 }
