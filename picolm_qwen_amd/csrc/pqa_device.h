@@ -19,28 +19,27 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 
 // fp32 -> fp16 exactly as cpp/quant.hpp:102-135 rounds: the magnitude gets
-// half an fp16 ulp added and is truncated (nearest, ties away from zero).
-// Normal range: adding 0x1000 to the rebased magnitude lets a mantissa carry
-// ripple into the exponent, and exponent 31 with a zero mantissa is the
-// infinity the reference returns. fp32 zero/subnormal -> signed zero;
-// NaN -> sign|0x7E00.
+// half an fp16 ulp added and is truncated (nearest, ties away from zero;
+// |x| >= 2^16 -> infinity, |x| < 2^-25 -> signed zero, NaN -> sign|0x7E00).
+// Computed branch-free from the hardware conversion, which rounds to nearest
+// even with fp16 subnormals kept: the two differ only on an exact tie whose
+// truncated value is even (nearest even kept it; ties away takes the next
+// value up in magnitude), below the infinity range, and in the NaN bits.
+// sh is the number of significand bits the fp16 value drops (13 for normal
+// results, 14..24 for subnormal ones, clamped to 25 below them, where no tie
+// exists). Equal to the reference's bit procedure on all 2^32 inputs.
 __device__ __forceinline__ uint16_t f32_to_f16_ref(float f) {
     const uint32_t bits = __float_as_uint(f);
-    const uint32_t sign = (bits >> 16) & 0x8000u;
     const uint32_t be = (bits >> 23) & 0xFFu;
-    const uint32_t mant = bits & 0x7FFFFFu;
-    uint32_t h;
-    if (be >= 143u) {
-        h = (be == 255u && mant) ? 0x7E00u : 0x7C00u;
-    } else if (be >= 113u) {
-        h = ((bits & 0x7FFFFFFFu) - (112u << 23) + 0x1000u) >> 13;
-    } else if (be >= 102u) {
-        const uint32_t shift = 126u - be;
-        h = ((mant | 0x800000u) + (1u << (shift - 1u))) >> shift;
-    } else {
-        h = 0u;
-    }
-    return (uint16_t)(sign | h);
+    const uint32_t m1 = (bits & 0x7FFFFFu) | 0x800000u;  // significand with the hidden bit
+    const int sh = min(max(126 - (int)be, 13), 25);
+    const uint32_t half = 1u << (sh - 1);
+    const bool tie = (m1 & (2u * half - 1u)) == half;
+    const bool odd = (m1 >> sh) & 1u;
+    uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+    h += (tie && !odd && be < 143u) ? 1u : 0u;
+    if (be == 255u && (bits & 0x7FFFFFu)) h = ((bits >> 16) & 0x8000u) | 0x7E00u;
+    return (uint16_t)h;
 }
 
 // fp16 bits -> fp32: exact widening (the hardware conversion equals
