@@ -132,6 +132,7 @@ constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 16;  // head dims per combine workgroup (HD / 16 workgroups per head)
 constexpr int kMaxCombineSplits = 256;
 constexpr int kShortMaxTiles = 4;  // per-column workgroups: most tiles per wave (one split)
+constexpr int kLateWriter = 3;     // per-column workgroups: the history wave that adds the new row last
 
 // PVM: PV on MFMA (v_mfma_f32_16x16x16_f16). The score tile S[row][head] that
 // the score MFMA leaves in lane (g, n), registers r = rows 4g + r of head n, is
@@ -148,14 +149,19 @@ constexpr int kShortMaxTiles = 4;  // per-column workgroups: most tiles per wave
 // 6.97 us; with shorter histories the new-row wave, third on its SIMD, ends
 // later than a history wave doing it would). Raising its issue priority
 // (1 or 2) measured slower: it then delays the two history waves beside it.
+// LW: history wave kLateWriter appends the new row after its own rows, at
+// issue priority 2 (per-column launches of 1 or 2 tiles per wave, including
+// the owner split of long histories): Qwen2.5-0.5B sweep 7.28 -> 7.11 us;
+// with 4 tiles per wave it measured slower than XW (C1 6.20 -> 6.46 us).
 template <bool XW>
 constexpr int decode_threads() {
     return 64 * (kDecodeWaves + (XW ? 1 : 0));
 }
 
-template <int HD, int G, bool PVM, int NT, bool PF, bool XW>
+template <int HD, int G, bool PVM, int NT, bool PF, bool XW, bool LW>
 __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const DecodeArgs a) {
     static_assert(!XW || PVM, "the new-row wave serves per-column workgroups");
+    static_assert(!LW || (PVM && !XW), "the late writer serves per-column workgroups");
     constexpr int NW = kDecodeWaves;  // history waves
     constexpr int NT_THREADS = decode_threads<XW>();
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const bool owner = split == a.nsplit - 1;
     // the wave that adds column c's new row: the new-row wave, else the
     // column's first history wave
-    const bool writer = owner && (XW ? w == NW : active && sb == 0);
+    const bool writer = owner && (XW ? w == NW : active && sb == (LW ? kLateWriter : 0));
     // column c = (KV head, chunk of at most G query heads)
     const int kvh = (ybase + c) / a.nchunk;
     const int hc = ybase + c - kvh * a.nchunk;
@@ -277,12 +283,49 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     pin(sn);
     PQA_STAMP(kStIssued + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
 
+    // The new K/V row of column c: K normed in the reference's summation
+    // order (cpp/tensor.hpp:146-176: quad j sums x[j], x[j+4], ...
+    // sequentially), rotated and rounded to fp16 as the reference does,
+    // stored once per KV head (chunk 0); the rounded V and the row's scores
+    // against the column's (normed, rotated, scaled) q heads kept for the merge.
+    auto new_row = [&]() {
+        if (a.qn) {
+            float* kr = skr[XW ? 0 : w];
+            if (lane < H4) ((float4*)kr)[t] = vk;
+            wave_sync();
+            const float sc = rms_scale_ref_quad<HD>(kr, lane & 3);
+            vk = float4{rms_apply(vk.x, sc, wk.x), rms_apply(vk.y, sc, wk.y), rms_apply(vk.z, sc, wk.z),
+                        rms_apply(vk.w, sc, wk.w)};
+        }
+        vk = rope_lanes<HD>(vk, a.rope, t, cs, sn);
+        const uint16_t kb0 = f32_to_f16_ref(vk.x), kb1 = f32_to_f16_ref(vk.y);
+        const uint16_t kb2 = f32_to_f16_ref(vk.z), kb3 = f32_to_f16_ref(vk.w);
+        const uint16_t vb0 = f32_to_f16_ref(vv.x), vb1 = f32_to_f16_ref(vv.y);
+        const uint16_t vb2 = f32_to_f16_ref(vv.z), vb3 = f32_to_f16_ref(vv.w);
+        if (hc == 0 && lane < H4) {
+            const size_t off = (size_t)a.pos * a.kv_dim + (size_t)kvh * HD + 4 * t;
+            *(u32x2*)(a.kc + off) = u32x2{kb0 | ((uint32_t)kb1 << 16), kb2 | ((uint32_t)kb3 << 16)};
+            *(u32x2*)(a.vc + off) = u32x2{vb0 | ((uint32_t)vb1 << 16), vb2 | ((uint32_t)vb3 << 16)};
+        }
+        if (lane < H4)
+            ((float4*)s_vnew[c])[t] = float4{f16_bits_to_f32(vb0), f16_bits_to_f32(vb1), f16_bits_to_f32(vb2),
+                                             f16_bits_to_f32(vb3)};
+        const float k0 = f16_bits_to_f32(kb0), k1 = f16_bits_to_f32(kb1);
+        const float k2 = f16_bits_to_f32(kb2), k3 = f16_bits_to_f32(kb3);
+#pragma unroll
+        for (int r = 0; r < QL; r++) {
+            float d = vq[r].x * k0 + vq[r].y * k1 + vq[r].z * k2 + vq[r].w * k3;
+            d = group_sum<H4>(d);
+            const int hh = (lane + 64 * r) / H4;
+            if (t == 0 && hh < Gc) s_new[c][hh] = d;
+        }
+        wave_sync();
+    };
+
     float* q_lds = sq[min(w, NW - 1)];
     if (active || writer) {
-        // QK-RMSNorm. q only feeds scores: an fp32 tree sum over the head's
-        // H4 lanes. K is stored, so its scale follows the reference's
-        // summation order (cpp/tensor.hpp:146-176): quad j sums x[j], x[j+4],
-        // ... sequentially; only the wave that appends the new row needs it.
+        // QK-RMSNorm of q: q only feeds scores, an fp32 tree sum over the
+        // head's H4 lanes.
         if (a.qn) {
 #pragma unroll
             for (int r = 0; r < QL; r++) {
@@ -291,14 +334,6 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
                 const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
                 vq[r] = float4{rms_apply(vq[r].x, sc, wq.x), rms_apply(vq[r].y, sc, wq.y),
                                rms_apply(vq[r].z, sc, wq.z), rms_apply(vq[r].w, sc, wq.w)};
-            }
-            if (writer) {
-                float* kr = skr[XW ? 0 : w];
-                if (lane < H4) ((float4*)kr)[t] = vk;
-                wave_sync();
-                const float sc = rms_scale_ref_quad<HD>(kr, lane & 3);
-                vk = float4{rms_apply(vk.x, sc, wk.x), rms_apply(vk.y, sc, wk.y), rms_apply(vk.z, sc, wk.z),
-                            rms_apply(vk.w, sc, wk.w)};
             }
         }
 #pragma unroll
@@ -312,36 +347,13 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
             const int i = lane + 64 * r;
             if (active && i < Gc * H4) ((float4*)(q_lds + (i / H4) * QS))[t] = vq[r];
         }
-        PQA_STAMP(kStNewRow0, writer && lane == 0);
-        if (writer) {
-            // new K/V row: rotate, round to fp16 as the reference does, store
-            // once per KV head (chunk 0), keep the rounded values for the merge
-            vk = rope_lanes<HD>(vk, a.rope, t, cs, sn);
-            const uint16_t kb0 = f32_to_f16_ref(vk.x), kb1 = f32_to_f16_ref(vk.y);
-            const uint16_t kb2 = f32_to_f16_ref(vk.z), kb3 = f32_to_f16_ref(vk.w);
-            const uint16_t vb0 = f32_to_f16_ref(vv.x), vb1 = f32_to_f16_ref(vv.y);
-            const uint16_t vb2 = f32_to_f16_ref(vv.z), vb3 = f32_to_f16_ref(vv.w);
-            if (hc == 0 && lane < H4) {
-                const size_t off = (size_t)a.pos * a.kv_dim + (size_t)kvh * HD + 4 * t;
-                *(u32x2*)(a.kc + off) = u32x2{kb0 | ((uint32_t)kb1 << 16), kb2 | ((uint32_t)kb3 << 16)};
-                *(u32x2*)(a.vc + off) = u32x2{vb0 | ((uint32_t)vb1 << 16), vb2 | ((uint32_t)vb3 << 16)};
-            }
-            if (lane < H4)
-                ((float4*)s_vnew[c])[t] = float4{f16_bits_to_f32(vb0), f16_bits_to_f32(vb1), f16_bits_to_f32(vb2),
-                                                 f16_bits_to_f32(vb3)};
-            const float k0 = f16_bits_to_f32(kb0), k1 = f16_bits_to_f32(kb1);
-            const float k2 = f16_bits_to_f32(kb2), k3 = f16_bits_to_f32(kb3);
-#pragma unroll
-            for (int r = 0; r < QL; r++) {
-                float d = vq[r].x * k0 + vq[r].y * k1 + vq[r].z * k2 + vq[r].w * k3;
-                d = group_sum<H4>(d);
-                const int hh = (lane + 64 * r) / H4;
-                if (t == 0 && hh < Gc) s_new[c][hh] = d;
-            }
+        if (!LW && writer) {
+            PQA_STAMP(kStNewRow0, lane == 0);
+            new_row();
+            PQA_STAMP(kStNewRow1, lane == 0);
         }
     }
     wave_sync();
-    PQA_STAMP(kStNewRow1, writer && lane == 0);
     PQA_STAMP(kStQReady + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
 
     // ---------------- wave loop over history rows ----------------
@@ -497,6 +509,18 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     }
 
     PQA_STAMP(kStLoop1 + (threadIdx.x >> 6), (threadIdx.x & 63) == 0);
+    if constexpr (LW) {
+        // the late writer: the new row after its own history rows, at the
+        // highest issue priority (the younger wave of its SIMD may still be
+        // in its loop)
+        if (writer) {
+            PQA_STAMP(kStNewRow0, lane == 0);
+            __builtin_amdgcn_s_setprio(2);
+            new_row();
+            __builtin_amdgcn_s_setprio(0);
+            PQA_STAMP(kStNewRow1, lane == 0);
+        }
+    }
     // ---------------- merge the four lane groups, then write the wave partial ----------------
     // Cross-lane sums by DPP / permlane swaps: lane groups differ in lane bits
     // 4 and 5; with HD 64 the two V rows of a lane group differ in bit 3.
@@ -773,12 +797,12 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
 // heads per column made the VALU PV the bound there), with 1, 2 or 4 tiles per
 // wave (4: two in flight, two iterations); whole-row workgroups stream HBM and
 // keep the VALU PV.
-template <int HD, bool PVM, int NT, bool PF, bool XW = false>
+template <int HD, bool PVM, int NT, bool PF, bool XW = false, bool LW = false>
 static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
     switch (G) {
 #define PQA_CASE(GG) \
     case GG:                                                                                                   \
-        hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF, XW>), grid, dim3(decode_threads<XW>()), 0, st, a); \
+        hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF, XW, LW>), grid, dim3(decode_threads<XW>()), 0, st, a); \
         break;
         PQA_CASE(1) PQA_CASE(2) PQA_CASE(3) PQA_CASE(4) PQA_CASE(5) PQA_CASE(6) PQA_CASE(7) PQA_CASE(8)
 #undef PQA_CASE
@@ -791,9 +815,9 @@ template <int HD>
 static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 grid, hipStream_t st) {
     hipError_t le = hipErrorInvalidValue;
     if (a.cpw != 1) le = launch_decode_pv<HD, false, kDecodeTiles, true>(a, G, grid, st);
-    else if (tiles == 1) le = launch_decode_pv<HD, true, 1, false>(a, G, grid, st);
-    else if (tiles == 2) le = launch_decode_pv<HD, true, 2, false>(a, G, grid, st);
-    else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true, true>(a, G, grid, st);  // one split
+    else if (tiles == 1) le = launch_decode_pv<HD, true, 1, false, false, true>(a, G, grid, st);
+    else if (tiles == 2) le = launch_decode_pv<HD, true, 2, false, false, true>(a, G, grid, st);
+    else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true, true, false>(a, G, grid, st);  // one split
     if (le != hipSuccess) return le;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
