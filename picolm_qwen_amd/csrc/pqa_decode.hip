@@ -149,10 +149,13 @@ constexpr int kLateWriter = 3;     // per-column workgroups: the history wave th
 // 6.97 us; with shorter histories the new-row wave, third on its SIMD, ends
 // later than a history wave doing it would). Raising its issue priority
 // (1 or 2) measured slower: it then delays the two history waves beside it.
-// LW: history wave kLateWriter appends the new row after its own rows, at
-// issue priority 2 (per-column launches of 1 or 2 tiles per wave, including
-// the owner split of long histories): Qwen2.5-0.5B sweep 7.28 -> 7.11 us;
-// with 4 tiles per wave it measured slower than XW (C1 6.20 -> 6.46 us).
+// LW: the writer appends the new row after its own history rows, at issue
+// priority 2: in per-column launches of 1 or 2 tiles per wave (including the
+// owner split of long histories) history wave kLateWriter (Qwen2.5-0.5B sweep
+// 7.28 -> 7.11 us; with 4 tiles per wave it measured slower than XW, C1 6.20
+// -> 6.46 us), in whole-row launches the first wave of each column of the
+// owner split, whose loads then start with everyone else's (C3 26.03 ->
+// 25.91 us, Qwen3-1.7B at ctx 8192 13.77 -> 13.47 us, C5 unchanged).
 template <bool XW>
 constexpr int decode_threads() {
     return 64 * (kDecodeWaves + (XW ? 1 : 0));
@@ -161,7 +164,7 @@ constexpr int decode_threads() {
 template <int HD, int G, bool PVM, int NT, bool PF, bool XW, bool LW>
 __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const DecodeArgs a) {
     static_assert(!XW || PVM, "the new-row wave serves per-column workgroups");
-    static_assert(!LW || (PVM && !XW), "the late writer serves per-column workgroups");
+    static_assert(!(LW && XW), "one new-row writer");
     constexpr int NW = kDecodeWaves;  // history waves
     constexpr int NT_THREADS = decode_threads<XW>();
     constexpr int KS = HD / 32;       // MFMA k-steps over the head dim
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const bool owner = split == a.nsplit - 1;
     // the wave that adds column c's new row: the new-row wave, else the
     // column's first history wave
-    const bool writer = owner && (XW ? w == NW : active && sb == (LW ? kLateWriter : 0));
+    const bool writer = owner && (XW ? w == NW : active && sb == (LW && PVM ? kLateWriter : 0));
     // column c = (KV head, chunk of at most G query heads)
     const int kvh = (ybase + c) / a.nchunk;
     const int hc = ybase + c - kvh * a.nchunk;
@@ -814,7 +817,7 @@ static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStr
 template <int HD>
 static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 grid, hipStream_t st) {
     hipError_t le = hipErrorInvalidValue;
-    if (a.cpw != 1) le = launch_decode_pv<HD, false, kDecodeTiles, true>(a, G, grid, st);
+    if (a.cpw != 1) le = launch_decode_pv<HD, false, kDecodeTiles, true, false, true>(a, G, grid, st);
     else if (tiles == 1) le = launch_decode_pv<HD, true, 1, false, false, true>(a, G, grid, st);
     else if (tiles == 2) le = launch_decode_pv<HD, true, 2, false, false, true>(a, G, grid, st);
     else if (tiles == 4) le = launch_decode_pv<HD, true, 2, true, true, false>(a, G, grid, st);  // one split
