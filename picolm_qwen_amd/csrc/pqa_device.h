@@ -21,25 +21,20 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 // fp32 -> fp16 exactly as cpp/quant.hpp:102-135 rounds: the magnitude gets
 // half an fp16 ulp added and is truncated (nearest, ties away from zero;
 // |x| >= 2^16 -> infinity, |x| < 2^-25 -> signed zero, NaN -> sign|0x7E00).
-// Computed branch-free from the hardware conversion, which rounds to nearest
-// even with fp16 subnormals kept: the two differ only on an exact tie whose
-// truncated value is even (nearest even kept it; ties away takes the next
-// value up in magnitude), below the infinity range, and in the NaN bits.
-// sh is the number of significand bits the fp16 value drops (13 for normal
-// results, 14..24 for subnormal ones, clamped to 25 below them, where no tie
-// exists). Equal to the reference's bit procedure on all 2^32 inputs.
+// Computed branch-free with the hardware conversion, which rounds to nearest
+// even with fp16 subnormals kept: when the first bit the fp16 value drops
+// (bit sh1 of the significand with its hidden bit: 12 for normal results,
+// 13..23 for subnormal ones, clamped to 24 below them, where it is 0) is
+// set, fp32 bit 0 is set too, which turns an exact tie into "above half"
+// and changes no other rounding; NaN gets the reference's bits. Equal to
+// the reference's bit procedure on all 2^32 inputs.
 __device__ __forceinline__ uint16_t f32_to_f16_ref(float f) {
     const uint32_t bits = __float_as_uint(f);
     const uint32_t be = (bits >> 23) & 0xFFu;
+    const int sh1 = min(max(125 - (int)be, 12), 24);
     const uint32_t m1 = (bits & 0x7FFFFFu) | 0x800000u;  // significand with the hidden bit
-    const int sh = min(max(126 - (int)be, 13), 25);
-    const uint32_t half = 1u << (sh - 1);
-    const bool tie = (m1 & (2u * half - 1u)) == half;
-    const bool odd = (m1 >> sh) & 1u;
-    uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
-    h += (tie && !odd && be < 143u) ? 1u : 0u;
-    if (be == 255u && (bits & 0x7FFFFFu)) h = ((bits >> 16) & 0x8000u) | 0x7E00u;
-    return (uint16_t)h;
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bits | ((m1 >> sh1) & 1u)));
+    return (be == 255u && (bits & 0x7FFFFFu)) ? (uint16_t)(((bits >> 16) & 0x8000u) | 0x7E00u) : h;
 }
 
 // fp16 bits -> fp32: exact widening (the hardware conversion equals
