@@ -695,7 +695,7 @@ def summarize_pmc(fetch_dir, write_dir):
             if r.get("Counter_Name") != counter:
                 continue
             name = r["Kernel_Name"]
-            key = ("copy" if "neg_kernel" in name else "decode" if "decode_kernel<128, 4>" in name
+            key = ("copy" if "neg_kernel" in name else "decode" if re.search(r"decode_kernel<128, 4[,>]", name)
                    else "combine" if "decode_combine_kernel<128>" in name else None)
             if key:
                 groups.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
