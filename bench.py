@@ -954,6 +954,42 @@ def phase_stamps(cases=None, reps=7):
     return "\n".join(lines)
 
 
+def sdpa_compare(reps=50):
+    """torch's scaled_dot_product_attention on the Qwen3-4B prefill shape
+    (1 x 32 heads x 2048 tokens x 128, causal, the 8 KV heads repeated),
+    fp16 and bf16, per backend that this torch offers: the vendor attention
+    beside which prefill_attn_kernel is measured (event-timed, µs per call)."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import sdpa_kernel, SDPBackend
+    dev = torch.device("cuda:0")
+    b, h, hk, s, d = 1, 32, 8, 2048, 128
+    flops = 4 * b * h * d * (s * (s + 1) / 2)
+    lines = []
+    for dt in (torch.float16, torch.bfloat16):
+        q = torch.randn(b, h, s, d, device=dev, dtype=dt)
+        k = torch.randn(b, hk, s, d, device=dev, dtype=dt).repeat_interleave(h // hk, dim=1).contiguous()
+        v = torch.randn(b, hk, s, d, device=dev, dtype=dt).repeat_interleave(h // hk, dim=1).contiguous()
+        for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+            try:
+                with sdpa_kernel(be):
+                    for _ in range(5):
+                        F.scaled_dot_product_attention(q, k, v, is_causal=True)
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(reps):
+                        F.scaled_dot_product_attention(q, k, v, is_causal=True)
+                    e1.record()
+                    torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                lines.append(f"[sdpa] {str(dt).split('.')[-1]:9s} {name:10s} {us:8.2f} us/layer "
+                             f"{flops / us / 1e6:7.1f} TFLOP/s")
+            except RuntimeError as ex:
+                lines.append(f"[sdpa] {str(dt).split('.')[-1]:9s} {name:10s} unavailable ({str(ex)[:80]})")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -973,7 +1009,12 @@ def main():
     ap.add_argument("--kernel", default="prefill_attn_kernel")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-phase decode and prefill timings from the stamped build (libpqa_stamps.so)")
+    ap.add_argument("--sdpa-compare", action="store_true",
+                    help="torch scaled_dot_product_attention on the Qwen3-4B prefill shape, for comparison")
     args = ap.parse_args()
+    if args.sdpa_compare:
+        print(sdpa_compare(), flush=True)
+        return
     if args.phase_stamps:
         print(phase_stamps(), flush=True)
         print(prefill_phase_stamps(), flush=True)
