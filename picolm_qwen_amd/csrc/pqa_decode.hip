@@ -14,10 +14,10 @@
 // per workgroup costs ~15 % of bandwidth). K/V loads are non-temporal (the
 // cache is read once per step) and run two 16-row tiles ahead, with row
 // indices clamped to the wave's range so no load sits behind a branch.
-// The last split also owns the new row: it applies the QK-norm and RoPE,
-// rounds K and V to fp16 with the reference's rounding, stores them at row
-// pos and adds that row's softmax term itself, so no workgroup reads a row
-// written in the same launch.
+// The last split also owns the new row: one of its waves (see XW and LW
+// below) applies the QK-norm and RoPE, rounds K and V to fp16 with the
+// reference's rounding, stores them at row pos and adds that row's softmax
+// term itself, so no workgroup reads a row written in the same launch.
 //
 // Inside a wave, per 16-row tile:
 //   scores  S[16 rows][16 cols] = K_tile x Q^T on v_mfma_f32_16x16x32_f16;
@@ -202,8 +202,9 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const int c = active ? w % cols : 0;
     const int sb = active ? w / cols : 0;
     const bool owner = split == a.nsplit - 1;
-    // the wave that adds column c's new row: the new-row wave, else the
-    // column's first history wave
+    // the wave that adds column c's new row: the new-row wave (XW), history
+    // wave kLateWriter (LW, per-column workgroups), else the column's first
+    // history wave (after its rows with LW, before them without)
     const bool writer = owner && (XW ? w == NW : active && sb == (LW && PVM ? kLateWriter : 0));
     // column c = (KV head, chunk of at most G query heads)
     const int kvh = (ybase + c) / a.nchunk;
