@@ -20,6 +20,12 @@ CASES = [
     ("qwen25_pos1", 14, 2, 64, 64, 0, 1e6, False, 1, 0.0),
     ("qwen25_pos77", 14, 2, 64, 128, 0, 1e6, False, 77, 0.0),
     ("qwen3_1p7b_pos1000", 16, 8, 128, 1024, 0, 1e6, True, 1000, 0.0),
+    # per-column splits of 128 rows; the owner split holds 40 rows, so the
+    # wave that adds the new row after its own rows (wave 3) has none
+    ("qwen25_pos936_idle_late_writer", 14, 2, 64, 1024, 0, 1e6, True, 936, 0.0),
+    # whole-row workgroups of 4 columns x 2 waves, 32-row splits; the owner
+    # split's first waves add the new row after their 16 rows
+    ("qwen3_1p7b_pos2000_whole_rows", 16, 8, 128, 2048, 0, 1e6, True, 2000, 0.0),
     ("qwen3_8b_outliers_pos4095", 32, 8, 128, 4096, 0, 1e6, True, 4095, 0.01),
     ("g16_two_chunks", 32, 2, 128, 600, 0, 1e6, True, 555, 0.0),
     ("interleaved_g1", 8, 8, 64, 300, 2, 1e4, False, 299, 0.0),
