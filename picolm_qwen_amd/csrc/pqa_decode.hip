@@ -544,23 +544,40 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
         const float M = max_x32(max_x16(m_run));
         const float e = (m_run == NEG_INF) ? 0.0f : fast_exp2(m_run - M);
         const float l = sum_x32(sum_x16(l_run * e));
+        // The 8 dims of a lane are summed over the four lane groups by a
+        // reduce-scatter: permlane32_swap(a, b) + its pair leaves a's sums over
+        // lane ^ 32 in the lower half and b's in the upper; permlane16_swap
+        // likewise over lane ^ 16 with odd and even rows. Lane group g ends
+        // with dims 2 g and 2 g + 1 (6 swaps and 6 adds instead of 16 and 16).
+        float2 part[AG];
 #pragma unroll
         for (int h = 0; h < AG; h++) {
             const float eh = row_bcast(e, h);
+            unsigned x[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                float x = acc[h][k] * eh;
-                if constexpr (RPG == 2) x = x + dpp_f<kDppXor8>(x);
-                acc[h][k] = sum_x32(sum_x16(x));
+                float xv = acc[h][k] * eh;
+                if constexpr (RPG == 2) xv = xv + dpp_f<kDppXor8>(xv);
+                x[k] = __builtin_bit_cast(unsigned, xv);
             }
-        }
-        if (lane < LPR) {
+            unsigned u[4];
 #pragma unroll
-            for (int h = 0; h < AG; h++) {
-                float* dst = q_lds + h * QS + vdim;
-                *(float4*)dst = float4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-                *(float4*)(dst + 4) = float4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            for (int k = 0; k < 4; k++) {
+                const auto r = __builtin_amdgcn_permlane32_swap(x[k], x[k + 4], false, false);
+                u[k] = __builtin_bit_cast(unsigned, __builtin_bit_cast(float, (unsigned)r[0]) +
+                                                        __builtin_bit_cast(float, (unsigned)r[1]));
             }
+            float y[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const auto r = __builtin_amdgcn_permlane16_swap(u[k], u[k + 2], false, false);
+                y[k] = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+            }
+            part[h] = float2{y[0], y[1]};
+        }
+        if (n < LPR) {
+#pragma unroll
+            for (int h = 0; h < AG; h++) *(float2*)(q_lds + h * QS + vdim + 2 * grp) = part[h];
         }
         if (lane < G) {
             wm[w][lane] = M;
