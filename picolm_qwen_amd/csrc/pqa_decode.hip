@@ -131,6 +131,7 @@ constexpr int kDecodeTiles = 2;  // whole-row workgroups: 16-row K/V tiles in fl
 constexpr int kCombineThreads = 256;
 constexpr int kCombineDims = 16;  // head dims per combine workgroup (HD / 16 workgroups per head)
 constexpr int kMaxCombineSplits = 256;
+constexpr int kSmallCombineSplits = 32;  // up to this many splits the merge runs one wave per workgroup
 constexpr int kShortMaxTiles = 4;  // per-column workgroups: most tiles per wave (one split)
 constexpr int kLateWriter = 3;     // per-column workgroups: the history wave that adds the new row last
 
@@ -729,6 +730,58 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const f
     }
 }
 
+// The same merge for at most kSmallCombineSplits splits (the per-column
+// launches of short histories): one wave per (head, column, 16-dim slice),
+// lane (split group sg = lane / 4, float4 d4 = lane % 4) on splits sg and
+// sg + 16, lane s on the (max, sum) of split s; every reduction stays in the
+// wave, with no LDS and no barrier.
+template <int HD>
+__global__ __launch_bounds__(64) void decode_combine_wave_kernel(const float* __restrict__ part_acc,
+                                                                 const float* __restrict__ part_ml,
+                                                                 float* __restrict__ out, int G, int g, int nchunk,
+                                                                 int nsplit) {
+    constexpr int D4 = kCombineDims / 4;           // float4s per slice
+    constexpr int SG = 64 / D4;                    // split groups
+    constexpr int U = kSmallCombineSplits / SG;    // splits per lane
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    static_assert(kSmallCombineSplits <= 64, "one lane per split for the (max, sum) pairs");
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x, y = blockIdx.y, dslice = blockIdx.z;
+    const int kvh = y / nchunk, hc = y - kvh * nchunk;
+    const int Gc = min(G, g - hc * G);
+    if (h >= Gc) return;
+    const float* pml = part_ml + ((size_t)y * nsplit * G + h) * 2;
+    const int d4 = lane % D4, sg = lane / D4;
+    const floatx4* src = (const floatx4*)(part_acc + ((size_t)y * nsplit * G + h) * HD + kCombineDims * dslice) + d4;
+    const size_t sstride = (size_t)G * HD / 4;
+
+    const float2 ml = *(const float2*)(pml + (size_t)min(lane, nsplit - 1) * G * 2);
+    floatx4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = src[(size_t)min(sg + u * SG, nsplit - 1) * sstride];
+    const float mloc = lane < nsplit ? ml.x : NEG_INF;
+    const float M = group_max<64>(mloc);
+    const float wt = lane < nsplit ? fast_exp2(mloc - M) : 0.0f;
+    const float L = group_sum<64>(wt * ml.y);
+    floatx4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const float ws = __shfl(wt, sg + u * SG);
+        if (sg + u * SG < nsplit) A += ws * v[u];
+    }
+    // sum over the split groups (lane bits 2..5), as in decode_combine_kernel
+    static_assert(D4 == 4, "the cross-lane sum below covers lane bits 2..5");
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float x = A[k];
+        x = x + dpp_f<kDppRor4>(x);
+        x = x + dpp_f<kDppXor8>(x);
+        A[k] = sum_x32(sum_x16(x));
+    }
+    if (lane < D4)
+        ((floatx4*)(out + (size_t)(kvh * g + hc * G + h) * HD + kCombineDims * dslice))[lane] = A * (1.0f / L);
+}
+
 void decode_split(const pqa_ctx* ctx, int hist, int max_splits, int* rows_per_split, int* nsplit, int* cols_per_wg,
                   int* tiles) {
     const int ny = ctx->n_kv_heads * ctx->n_chunk;
@@ -843,7 +896,11 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, int G, int tiles, dim3 g
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
     if (a.nsplit > kMaxCombineSplits) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(kCombineThreads), 0, st,
+    if (a.nsplit <= kSmallCombineSplits)
+        hipLaunchKernelGGL(decode_combine_wave_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(64), 0, st,
+                           a.part_acc, a.part_ml, a.out, G, a.g, a.nchunk, a.nsplit);
+    else
+        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(G, a.ny, HD / kCombineDims), dim3(kCombineThreads), 0, st,
                        a.part_acc,
                        a.part_ml, a.out, G, a.g, a.nchunk, a.nsplit);
     return hipGetLastError();
