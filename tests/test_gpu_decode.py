@@ -32,6 +32,10 @@ CASES = [
     ("block8_g3_qknorm", 12, 4, 128, 200, 1, 1e4, True, 150, 0.0),
     ("g5_pos_65", 10, 2, 64, 100, 0, 1e6, True, 65, 0.0),
     ("two_column_groups", 32, 16, 64, 400, 0, 1e6, False, 333, 0.0),
+    # whole-row workgroups whose column count is not a power of two: 3
+    # columns x 2 waves (waves 6, 7 idle), and 5 columns x 1 wave
+    ("whole_rows_three_columns", 6, 3, 128, 4096, 0, 1e6, True, 4000, 0.0),
+    ("whole_rows_five_columns", 20, 5, 64, 2048, 0, 1e6, False, 2000, 0.0),
 ]
 
 
