@@ -21,8 +21,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: the K row written to the cache must round like the
 # reference (no fused multiply-add in RMSNorm or RoPE); kernels that want an
 # FMA call fmaf() explicitly. Packed fp32 instructions are disabled.
+# -amdgpu-kernarg-preload-count: the leading scalar kernel arguments (up to
+# 14 words) arrive in SGPRs at dispatch, not by a load from the argument
+# segment; the code object keeps a fallback prologue that loads them.
 CFLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-mllvm", "-amdgpu-kernarg-preload-count=16",
           "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 
 

@@ -62,6 +62,8 @@ extern "C" int pqa_create(pqa_ctx** out, int n_layers, int max_seq_len, int n_he
         return set_err(nullptr, PQA_ERR_ARG, "pqa_create: n_heads must be a multiple of n_kv_heads");
     if (head_dim <= 0 || head_dim > pqa::kMaxHeadDim || head_dim % 2 != 0)
         return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: head_dim must be even and at most 512");
+    if (n_heads / n_kv_heads > 0xFFFF)  // the decode launch packs it in 16 bits
+        return set_err(nullptr, PQA_ERR_UNSUPPORTED, "pqa_create: more than 65535 query heads per KV head");
     if (rope_style < 0 || rope_style > 2) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: bad rope_style");
     if (!rope_cos || !rope_sin) return set_err(nullptr, PQA_ERR_ARG, "pqa_create: RoPE tables are NULL");
 

@@ -162,8 +162,25 @@ constexpr int decode_threads() {
     return 64 * (kDecodeWaves + (XW ? 1 : 0));
 }
 
+// The fields of the q, RoPE and K/V tile addresses come first, as scalar
+// arguments (packed = g | rope << 16 | QK-norm << 18): built with
+// -amdgpu-kernarg-preload-count, the dispatch puts these 14 words in SGPRs
+// before the first instruction; only the struct (passed by reference into
+// the argument segment, never preloaded) is loaded, in one round trip at the
+// start. C1 5.91 -> 5.75 us, C3 25.77 -> 25.47 us with the combine launch,
+// whose arguments are all preloaded. Holding the struct's first use (where
+// the compiler waits for it) back behind the q and tile loads measured
+// slower: C1 6.10-6.16 us.
 template <int HD, int G, bool PVM, int NT, bool PF, bool XW, bool LW>
-__global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(uint16_t* kc, uint16_t* vc, const float* q,
+                                                                      const float* cosr, const float* sinr, int pos,
+                                                                      int rows_per_split, int kv_dim, int packed,
+                                                                      const DecodeArgs args) {
+    DecodeArgs a = args;
+    a.kc = kc, a.vc = vc, a.q = q, a.cosr = cosr, a.sinr = sinr;
+    a.pos = pos, a.rows_per_split = rows_per_split, a.kv_dim = kv_dim;
+    a.g = packed & 0xFFFF, a.nchunk = (a.g + 7) >> 3, a.rope = (packed >> 16) & 3;
+    const bool norm = (packed >> 18) & 1;
     static_assert(!XW || PVM, "the new-row wave serves per-column workgroups");
     static_assert(!(LW && XW), "one new-row writer");
     constexpr int NW = kDecodeWaves;  // history waves
@@ -195,7 +212,7 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int split = blockIdx.x;
-    const int ybase = blockIdx.y * a.cpw;
+    const int ybase = PVM ? (int)blockIdx.y : (int)blockIdx.y * a.cpw;
     PQA_STAMP(kStStart, threadIdx.x == 0);
     // Per-column workgroups (PVM) have one column, so the divisions below
     // fold away there (they sit on the path to the first loads: C1 6.06 ->
@@ -206,7 +223,9 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     const bool active = w < cols * sub;
     const int c = active ? w % cols : 0;
     const int sb = active ? w / cols : 0;
-    const bool owner = split == a.nsplit - 1;
+    // the last split (split == nsplit - 1 for nsplit = max(1, ceil(pos /
+    // rows_per_split)), which the launch checks), from preloaded arguments only
+    const bool owner = (split + 1) * a.rows_per_split >= a.pos;
     // the wave that adds column c's new row: the new-row wave (XW), history
     // wave kLateWriter (LW, per-column workgroups), else the column's first
     // history wave (after its rows with LW, before them without)
@@ -259,15 +278,15 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
         const int hh = min((lane + 64 * r) / H4, Gc - 1);
         vq[r] = ((const float4*)(a.q + (size_t)(h0 + hh) * HD))[t];
     }
-    float4 vk = ((const float4*)(a.k + (size_t)kvh * HD))[t];
-    float4 vv = ((const float4*)(a.v + (size_t)kvh * HD))[t];
-    const float* qn = a.qn ? a.qn : a.wpad;  // loads stay unconditional without a norm
-    const float* kn = a.kn ? a.kn : a.wpad + HD;
-    float4 wq = ((const float4*)qn)[t];
-    float4 wk = ((const float4*)kn)[t];
     const int ci = rope_angle_f4<HD>(a.rope, t);
     float4 cs = ((const float4*)a.cosr)[ci];
     float4 sn = ((const float4*)a.sinr)[ci];
+    float4 vk = ((const float4*)(a.k + (size_t)kvh * HD))[t];
+    float4 vv = ((const float4*)(a.v + (size_t)kvh * HD))[t];
+    const float* qn = norm ? a.qn : a.wpad;  // loads stay unconditional without a norm
+    const float* kn = norm ? a.kn : a.wpad + HD;
+    float4 wq = ((const float4*)qn)[t];
+    float4 wk = ((const float4*)kn)[t];
     // Per-column workgroups with history: every wave's small loads enter the
     // memory pipe before any wave's tiles; otherwise the older wave of each
     // SIMD queues its tiles ahead of the younger one's q, and the younger wave
@@ -298,7 +317,7 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     // stored once per KV head (chunk 0); the rounded V and the row's scores
     // against the column's (normed, rotated, scaled) q heads kept for the merge.
     auto new_row = [&]() {
-        if (a.qn) {
+        if (norm) {
             float* kr = skr[XW ? 0 : w];
             if (lane < H4) ((float4*)kr)[t] = vk;
             wave_sync();
@@ -335,7 +354,7 @@ __global__ __launch_bounds__(decode_threads<XW>()) void decode_kernel(const Deco
     if (active || writer) {
         // QK-RMSNorm of q: q only feeds scores, an fp32 tree sum over the
         // head's H4 lanes.
-        if (a.qn) {
+        if (norm) {
 #pragma unroll
             for (int r = 0; r < QL; r++) {
                 const float ss = group_sum<H4>(vq[r].x * vq[r].x + vq[r].y * vq[r].y + vq[r].z * vq[r].z +
@@ -877,10 +896,17 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
 // keep the VALU PV.
 template <int HD, bool PVM, int NT, bool PF, bool XW = false, bool LW = false>
 static hipError_t launch_decode_pv(const DecodeArgs& a, int G, dim3 grid, hipStream_t st) {
+    // the packed argument word, and the chunk count the kernel derives from g
+    // and the owner split the kernel derives from pos and rows_per_split
+    if (a.g < 1 || a.g > 0xFFFF || a.rope < 0 || a.rope > 3 || a.nchunk != (a.g + 7) / 8) return hipErrorInvalidValue;
+    if (a.rows_per_split < 1 || a.nsplit != std::max(1, (a.pos + a.rows_per_split - 1) / a.rows_per_split))
+        return hipErrorInvalidValue;
     switch (G) {
 #define PQA_CASE(GG) \
     case GG:                                                                                                   \
-        hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF, XW, LW>), grid, dim3(decode_threads<XW>()), 0, st, a); \
+        hipLaunchKernelGGL((decode_kernel<HD, GG, PVM, NT, PF, XW, LW>), grid, dim3(decode_threads<XW>()), 0, st, \
+                           a.kc, a.vc, a.q, a.cosr, a.sinr, a.pos, a.rows_per_split, a.kv_dim,                  \
+                           a.g | (a.rope << 16) | (a.qn ? 1 << 18 : 0), a);                                      \
         break;
         PQA_CASE(1) PQA_CASE(2) PQA_CASE(3) PQA_CASE(4) PQA_CASE(5) PQA_CASE(6) PQA_CASE(7) PQA_CASE(8)
 #undef PQA_CASE
