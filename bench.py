@@ -219,8 +219,9 @@ def host_entry_decode(cx, q, k, v, out, pos, steps):
     t = median_time(step, max(3, steps // 3))
     return {"entry": "pqa_decode_host", "us_per_layer": round(t * 1e6 / cx.n_layers, 2),
             "equals_device_entry": bool(np.array_equal(oh, want)),
-            "note": "the caller's pageable host buffers; the payload goes through the library's pinned staging "
-                    "buffer: one H2D copy, the decode, one D2H copy and a stream sync per call"}
+            "note": "the caller's pageable host buffers, copied by the CPU into and out of the library's pinned "
+                    "staging buffer, which the decode kernels read and write directly (no DMA copies); "
+                    "a stream sync per call"}
 
 
 def timed(torch, cx, fn, steps, warmup):

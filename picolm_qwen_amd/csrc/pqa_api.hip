@@ -259,6 +259,24 @@ static int run_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, c
     hipStream_t st = ctx->stream;
     const bool pinned = (in_floats + nq) * sizeof(float) <= kHostStageBytes;
     int rc = PQA_OK;
+    if (pinned && !prefill) {
+        // Decode reads q, k, v and writes out in the pinned staging buffer
+        // itself (host memory the device addresses directly): no DMA copies,
+        // the launches and one stream sync. The previous call ended with a
+        // stream sync, so the buffer is free.
+        if ((rc = ensure_hstage(ctx, in_floats + nq))) return rc;
+        float* h = ctx->hstage;
+        std::memcpy(h, q, nq * sizeof(float));
+        std::memcpy(h + nq, k, nkv * sizeof(float));
+        std::memcpy(h + nq + nkv, v, nkv * sizeof(float));
+        float* hd = nullptr;
+        rc = hip_check(ctx, hipHostGetDevicePointer((void**)&hd, h, 0), fn);
+        if (!rc) rc = pqa_decode(ctx, layer, pos, hd, hd + nq, hd + nq + nkv, hd + in_floats);
+        if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
+        else (void)hipStreamSynchronize(st);  // a failed call leaves no kernel using the buffer
+        if (!rc) std::memcpy(out, h + in_floats, nq * sizeof(float));
+        return rc;
+    }
     if (pinned) {
         // the previous call ended with a stream sync, so the buffer is free
         if ((rc = ensure_hstage(ctx, in_floats + nq))) return rc;
