@@ -45,6 +45,9 @@ def test_create_rejects_bad_shapes_before_any_device_call():
     assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 0, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
     assert L.pqa_create(C.byref(h), 1, 64, 6, 4, 64, 0, p, p) == _lib.PQA_ERR_ARG
     assert b"multiple" in L.pqa_last_error(None)
+    # more query heads per KV head than the decode launch's 16-bit field holds
+    assert L.pqa_create(C.byref(h), 1, 64, 65536, 1, 64, 0, p, p) == _lib.PQA_ERR_UNSUPPORTED
+    assert not h.value
     assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 64, 3, p, p) == _lib.PQA_ERR_ARG
     assert L.pqa_create(C.byref(h), 0, 64, 8, 2, 64, 0, p, p) == _lib.PQA_ERR_ARG
     assert L.pqa_create(C.byref(h), 1, 64, 8, 2, 64, 0, None, None) == _lib.PQA_ERR_ARG
