@@ -305,6 +305,24 @@ int pqa_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float 
  * fp32 summation order. */
 int pqa_set_decode_split(pqa_ctx* ctx, int rows_per_split);
 
+/*
+ * How the batched entry points (pqa_qkv_project_batch, pqa_prefill_x,
+ * pqa_prefill_block) project K and V.
+ * 1 (default): the attn_k and attn_v columns are computed in the reference's
+ *    own summation order (vec_dot, cpp/quant.hpp:297-356, as forward_batch
+ *    calls matmul_bias per token, cpp/model.hpp:503-546) on a VALU GEMM, so k
+ *    and v are bit-identical to pqa_qkv_project's and the cache rows a prompt
+ *    writes are the reference's bits (built without FMA contraction); q stays
+ *    on the split fp16 GEMM, within its error bound (q only feeds scores).
+ *    The first such call for a layer keeps its K/V rows as fp32, about
+ *    2 * kv_dim * n_embd * 4 bytes (plus n_embd / 8 floats per row for Q8_0),
+ *    until the weights are replaced.
+ * 0: all three on the split fp16 GEMM: faster, but a K or V element can land
+ *    one fp16 step away from the reference's.
+ * No counterpart in the reference, which has one order only.
+ */
+int pqa_set_batch_projection(pqa_ctx* ctx, int exact_kv);
+
 /* Prefill score precision.
  * 1 (default): q is carried as fp16 hi + lo (two MFMAs per k-step),
  *    fp32-level scores.

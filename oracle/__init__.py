@@ -114,6 +114,8 @@ def _bind(L):
     L.pqo_vec_dot.restype = C.c_float
     L.pqo_vec_dot.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_int]
     L.pqo_matmul_bias.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]
+    L.pqo_matmul_bias_tokens.argtypes = [_f32p, _f32p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int,
+                                         C.c_int, C.c_int]
     return L
 
 
@@ -313,6 +315,17 @@ def matmul_bias(x, w_raw, wtype, d, b_raw=None, btype=GGUF_NONE):
     out = np.empty(d, np.float32)
     if lib().pqo_matmul_bias(out, x, _vp(np.ascontiguousarray(w_raw)), wtype,
                              _vp(None if b_raw is None else np.ascontiguousarray(b_raw)), btype, x.size, d):
+        raise ValueError("unsupported type or shape")
+    return out
+
+
+def matmul_bias_tokens(x, w_raw, wtype, d, b_raw=None, btype=GGUF_NONE, n_threads=8):
+    """matmul_bias of every row of x [n_tok][n] -> [n_tok][d], rows split over threads."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], d), np.float32)
+    if lib().pqo_matmul_bias_tokens(out.reshape(-1), x.reshape(-1), x.shape[0], _vp(np.ascontiguousarray(w_raw)),
+                                    wtype, _vp(None if b_raw is None else np.ascontiguousarray(b_raw)), btype,
+                                    x.shape[1], d, n_threads):
         raise ValueError("unsupported type or shape")
     return out
 

@@ -147,6 +147,10 @@ int    pqo_dequant_row(int type, const void* src, float* dst, int n);
 float  pqo_vec_dot(int type, const void* row, const float* x, int n);
 int    pqo_matmul_bias(float* out, const float* x, const void* w, int wtype, const void* b, int btype,
                        int n, int d);
+/* pqo_matmul_bias for each of n_tok inputs x [n_tok][n] -> out [n_tok][d],
+ * rows split over n_threads (same bits per token). */
+int    pqo_matmul_bias_tokens(float* out, const float* x, int n_tok, const void* w, int wtype, const void* b,
+                              int btype, int n, int d, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -7,6 +7,8 @@
  * every product and sum rounds separately, in the reference's order on x86
  * (the SSE2 path of vec_dot_f32_f32).
  */
+#include <pthread.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "pqa_oracle.h"
@@ -175,5 +177,67 @@ int pqo_matmul_bias(float* out, const float* x, const void* w, int wtype, const 
         if (d > 16384 || pqo_dequant_row(btype, b, bias, d)) return -1;
         for (int i = 0; i < d; i++) out[i] = out[i] + bias[i];
     }
+    return 0;
+}
+
+/* matmul_bias for n_tok inputs x [n_tok][n] -> out [n_tok][d]: per token the
+ * same arithmetic as pqo_matmul_bias (forward_batch calls matmul_bias per
+ * token, cpp/model.hpp:503-546); a row is dequantized once for all tokens
+ * (dequantize_row is exact and does not depend on x), and rows are split over
+ * n_threads. */
+typedef struct {
+    float* out;
+    const float* x;
+    const uint8_t* w;
+    const float* bias;
+    size_t rb;
+    int n_tok, wtype, n, d, r0, r1;
+} mm_job;
+
+static void* mm_worker(void* arg) {
+    const mm_job* j = (const mm_job*)arg;
+    float* buf = (float*)malloc((size_t)j->n * sizeof(float));
+    for (int r = j->r0; r < j->r1 && buf; r++) {
+        const uint8_t* row = j->w + (size_t)r * j->rb;
+        const int direct = j->wtype == PQO_GGUF_F32 || j->wtype == PQO_GGUF_Q8_0;
+        if (!direct) pqo_dequant_row(j->wtype, row, buf, j->n);
+        for (int t = 0; t < j->n_tok; t++) {
+            const float* xt = j->x + (size_t)t * j->n;
+            float v = direct ? pqo_vec_dot(j->wtype, row, xt, j->n) : dot_f32(buf, xt, j->n);
+            if (j->bias) v = v + j->bias[r];
+            j->out[(size_t)t * j->d + r] = v;
+        }
+    }
+    free(buf);
+    return NULL;
+}
+
+int pqo_matmul_bias_tokens(float* out, const float* x, int n_tok, const void* w, int wtype, const void* b, int btype,
+                           int n, int d, int n_threads) {
+    const size_t rb = pqo_row_bytes(wtype, n);
+    if (!rb || n > 16384 || n_tok <= 0 || d <= 0) return -1;
+    float* bias = NULL;
+    if (btype != PQO_GGUF_NONE && b) {
+        bias = (float*)malloc((size_t)d * sizeof(float));
+        if (!bias || pqo_dequant_row(btype, b, bias, d)) {
+            free(bias);
+            return -1;
+        }
+    }
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > 64) n_threads = 64;
+    if (n_threads > d) n_threads = d;
+    mm_job jobs[64];
+    pthread_t th[64];
+    const int per = (d + n_threads - 1) / n_threads;
+    for (int t = 0; t < n_threads; t++) {
+        const int r0 = t * per, r1 = r0 + per < d ? r0 + per : d;
+        jobs[t] = (mm_job){out, x, (const uint8_t*)w, bias, rb, n_tok, wtype, n, d, r0, r1};
+        if (n_threads > 1) pthread_create(&th[t], NULL, mm_worker, &jobs[t]);
+    }
+    if (n_threads == 1) mm_worker(&jobs[0]);
+    else
+        for (int t = 0; t < n_threads; t++) pthread_join(th[t], NULL);
+    free(bias);
     return 0;
 }

@@ -15,7 +15,7 @@ LIB = os.path.join(PKG, "libpqa.so")
 # stamps at their phase boundaries (measurement only, bench.py --phase-stamps)
 STAMPS_LIB = os.path.join(PKG, "libpqa_stamps.so")
 SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip",
-           "pqa_gemm.hip", "pqa_general.hip"]
+           "pqa_gemm.hip", "pqa_general.hip", "pqa_exact.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: the K row written to the cache must round like the

@@ -209,6 +209,13 @@ class PicoAttention:
         fp16 q (faster; its score error grows with |q| |k|)."""
         check(lib().pqa_set_prefill_precision(self.handle, int(bool(split_q))), self.handle)
 
+    def set_batch_projection(self, exact_kv: bool) -> None:
+        """True (the default): the batched entry points compute K and V in the
+        reference's summation order (bit-exact cache rows) and q on the split
+        fp16 GEMM; False: all three on the split GEMM (faster; a K/V element can
+        land one fp16 step off)."""
+        check(lib().pqa_set_batch_projection(self.handle, int(bool(exact_kv))), self.handle)
+
     # -- the block ----------------------------------------------------------
     def set_qk_norm(self, layer: int, q_norm_w, k_norm_w) -> None:
         """Layer's attn_q_norm / attn_k_norm weights ([head_dim] each); None turns it off."""

@@ -192,19 +192,19 @@ struct ScatterArgs {
     int rows[3];
 };
 
-// Y [n_tok][total] holds q|k|v of every token scaled by 2^(s_w + s_x):
+// Y [n_tok][ld] holds q|k|v of every token scaled by 2^(s_w + s_x):
 // out_m[t][r] = Y[t][off_m + r] * 2^-(s_w + s_x), an exact rescale, then
-// out + b[r] (vec_add, cpp/tensor.hpp:410-420). Thread: 4 consecutive rows of
-// one token (rows of q and kv are multiples of 4).
-__global__ __launch_bounds__(256) void unscale_scatter_kernel(const float* __restrict__ Y, int total,
+// out + b[r] (vec_add, cpp/tensor.hpp:410-420), for the first ncols columns.
+// Thread: 4 consecutive rows of one token (rows of q and kv are multiples of 4).
+__global__ __launch_bounds__(256) void unscale_scatter_kernel(const float* __restrict__ Y, int ld, int ncols,
                                                               const float* __restrict__ w_inv,
                                                               const float* __restrict__ x_inv, const ScatterArgs a) {
     const int t = blockIdx.y;
     const int r = 4 * (blockIdx.x * 256 + threadIdx.x);
-    if (r >= total) return;
+    if (r >= ncols) return;
     const int m = r < a.rows[0] ? 0 : (r < a.rows[0] + a.rows[1] ? 1 : 2);
     const int rr = r - (m > 0 ? a.rows[0] : 0) - (m > 1 ? a.rows[1] : 0);
-    const floatx4 y = *(const floatx4*)(Y + (size_t)t * total + r);
+    const floatx4 y = *(const floatx4*)(Y + (size_t)t * ld + r);
     const floatx4 wi = *(const floatx4*)(w_inv + r);
     const float xi = x_inv[t];
     floatx4 o;
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void unscale_residual_kernel(const float* __re
     *xp = o;
 }
 
-static hipError_t launch_dequant(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s) {
+hipError_t launch_dequant_rows(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s) {
     const long long items = (long long)rows * ((n + 31) / 32);
     const dim3 grid((unsigned)((items + 255) / 256));
     switch (type) {
@@ -307,7 +307,7 @@ static int ensure_layer_split(pqa_ctx* ctx, int layer, const char* fn) {
     float* w_inv = (float*)((char*)buf + wb);
     size_t off = 0;
     for (int i = 0; i < 3; i++) {
-        hipError_t e = pqa::launch_dequant(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
+        hipError_t e = pqa::launch_dequant_rows(p.wtype[i], p.w[i], p.stride[i], rows[i], n, ctx->wf32, ctx->stream);
         if (e == hipSuccess) {
             pqa::launch_split2((const float*)ctx->wf32, rows[i], n, w3 + off * 2 * kh, kh, w_inv + off, ctx->stream);
             e = hipGetLastError();
@@ -331,7 +331,7 @@ static int ensure_layer_out_split(pqa_ctx* ctx, int layer, const char* fn) {
     if (int rc = ensure_batch(ctx, (size_t)rows * n, fn)) return rc;
     void* buf = nullptr;
     if (int rc = hip_check(ctx, hipMalloc(&buf, wb + up256((size_t)rows * 4)), fn)) return rc;
-    hipError_t e = pqa::launch_dequant(p.wtype[3], p.w[3], p.stride[3], rows, n, ctx->wf32, ctx->stream);
+    hipError_t e = pqa::launch_dequant_rows(p.wtype[3], p.w[3], p.stride[3], rows, n, ctx->wf32, ctx->stream);
     if (e == hipSuccess) {
         pqa::launch_split2((const float*)ctx->wf32, rows, n, (_Float16*)buf, kh, (float*)((char*)buf + wb),
                            ctx->stream);
@@ -343,6 +343,42 @@ static int ensure_layer_out_split(pqa_ctx* ctx, int layer, const char* fn) {
     }
     p.out_split = buf;
     return PQA_OK;
+}
+
+// The layer's attn_k and attn_v rows prepared for the reference-order
+// projection (pqa_exact.hip), made on the first call that needs them.
+static int ensure_layer_exact(pqa_ctx* ctx, int layer, const char* fn) {
+    auto& p = ctx->proj[layer];
+    if (p.exact) return PQA_OK;
+    const int n = p.n_embd, rows = (int)ctx->kv_dim;
+    const size_t fk = pqa::exact_matrix_floats(p.wtype[1], rows, n);
+    const size_t fv = pqa::exact_matrix_floats(p.wtype[2], rows, n);
+    float* buf = nullptr;
+    if (int rc = hip_check(ctx, hipMalloc(&buf, (fk + fv) * 4), fn)) return rc;
+    hipError_t e = pqa::prepare_exact_matrix(p.wtype[1], p.w[1], p.stride[1], rows, n, buf, ctx->stream);
+    if (e == hipSuccess) e = pqa::prepare_exact_matrix(p.wtype[2], p.w[2], p.stride[2], rows, n, buf + fk, ctx->stream);
+    if (int rc = hip_check(ctx, e, fn)) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(buf);
+        return rc;
+    }
+    p.exact = buf;
+    return PQA_OK;
+}
+
+// k[t * ldo + r] and v[t * ldo + r] = the attn_k / attn_v matmul_bias of token
+// t in the reference's order (pqa_exact.hip), bit-exact.
+static int exact_kv(pqa_ctx* ctx, int layer, int n_tok, const float* xb, float* k, float* v, int ldo, const char* fn) {
+    if (int rc = ensure_layer_exact(ctx, layer, fn)) return rc;
+    const auto& p = ctx->proj[layer];
+    const int n = p.n_embd, rows = (int)ctx->kv_dim;
+    const float* wk = p.exact;
+    const float* wv = p.exact + pqa::exact_matrix_floats(p.wtype[1], rows, n);
+    hipError_t e = pqa::launch_ordered_project(p.wtype[1], wk, rows, n, xb, n, n_tok, p.b[1], p.btype[1], k, ldo,
+                                               ctx->stream);
+    if (e == hipSuccess)
+        e = pqa::launch_ordered_project(p.wtype[2], wv, rows, n, xb, n, n_tok, p.b[2], p.btype[2], v, ldo, ctx->stream);
+    return hip_check(ctx, e, fn);
 }
 
 // Per call: X' [n_tok][2 k_half(n)] halfs, the inverse scales of X's rows, and
@@ -381,8 +417,10 @@ static int ensure_split(pqa_ctx* ctx, int n_tok, int n, size_t total, SplitBufs*
 
 // X' and the GEMM of one call: sb->y [n_tok][q_dim + 2 kv_dim] = X W^T, every
 // element scaled by 2^(s_w[c] + s_x[t]); *w_inv = the inverse column scales.
+// q_only: the GEMM covers the q columns alone (the reference-order projection
+// fills the k and v columns).
 static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, SplitBufs* sb, const float** w_inv,
-                      const char* fn) {
+                      const char* fn, bool q_only = false) {
     const int n = ctx->proj[layer].n_embd;
     if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     const auto& p = ctx->proj[layer];
@@ -393,9 +431,10 @@ static int batch_gemm(pqa_ctx* ctx, int layer, int n_tok, const float* xb, Split
     if (int rc = ensure_split(ctx, n_tok, n, total, sb, fn)) return rc;
     pqa::launch_split2(xb, n_tok, n, sb->x3, kh, sb->x_inv, ctx->stream);
     if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
-    // Y[n_tok][total] = X_hi W_hi^T + X_hi W_lo^T + X_lo W_hi^T
+    // Y[n_tok][total] = X_hi W_hi^T + X_hi W_lo^T + X_lo W_hi^T (the q rows come first)
+    const int ncols = q_only ? (int)ctx->q_dim : (int)total;
     return hip_check(ctx,
-                     pqa::launch_gemm_f16x3_nt(sb->x3, 2 * kh, w3, 2 * kh, sb->y, (int)total, n_tok, (int)total, kh,
+                     pqa::launch_gemm_f16x3_nt(sb->x3, 2 * kh, w3, 2 * kh, sb->y, (int)total, n_tok, ncols, kh,
                                                         ctx->stream),
                      fn);
 }
@@ -420,9 +459,12 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
                        "pqa_qkv_project_batch: n_heads * head_dim and n_kv_heads * head_dim must be multiples of 4");
     if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) != 0)
         return set_err(ctx, PQA_ERR_ARG, "pqa_qkv_project_batch: q, k and v must be 16-byte aligned");
+    const bool exact = ctx->batch_exact_kv != 0;
+    if (exact)  // the prepared K/V rows exist before any kernel of the call is queued
+        if (int rc = ensure_layer_exact(ctx, layer, fn)) return rc;
     SplitBufs sb;
     const float* w_inv = nullptr;
-    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn)) return rc;
+    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn, exact)) return rc;
     const auto& p = ctx->proj[layer];
     const size_t total = ctx->q_dim + 2 * ctx->kv_dim;
     pqa::ScatterArgs sa;
@@ -433,10 +475,12 @@ extern "C" int pqa_qkv_project_batch(pqa_ctx* ctx, int layer, int n_tok, const f
         sa.btype[i] = p.btype[i];
         sa.rows[i] = i == 0 ? (int)ctx->q_dim : (int)ctx->kv_dim;
     }
-    const unsigned gx = (unsigned)((total / 4 + 255) / 256);
+    const int ncols = exact ? (int)ctx->q_dim : (int)total;
+    const unsigned gx = (unsigned)((ncols / 4 + 255) / 256);
     hipLaunchKernelGGL(pqa::unscale_scatter_kernel, dim3(gx, n_tok), dim3(256), 0, ctx->stream, (const float*)sb.y,
-                       (int)total, w_inv, (const float*)sb.x_inv, sa);
-    return hip_check(ctx, hipGetLastError(), fn);
+                       (int)total, ncols, w_inv, (const float*)sb.x_inv, sa);
+    if (int rc = hip_check(ctx, hipGetLastError(), fn)) return rc;
+    return exact ? exact_kv(ctx, layer, n_tok, xb, k, v, (int)ctx->kv_dim, fn) : PQA_OK;
 }
 
 // The prompt path from the normed inputs: the GEMM result goes to the prefill
@@ -450,19 +494,27 @@ extern "C" int pqa_prefill_x(pqa_ctx* ctx, int layer, int start_pos, int n_tok, 
     if (((uintptr_t)out & 15) != 0) return set_err(ctx, PQA_ERR_ARG, "pqa_prefill_x: out must be 16-byte aligned");
     if (start_pos < 0 || (long long)start_pos + n_tok > ctx->max_seq_len)
         return set_err(ctx, PQA_ERR_RANGE, "pqa_prefill_x: positions past max_seq_len");
+    const bool exact = ctx->batch_exact_kv != 0;
+    if (exact)
+        if (int rc = ensure_layer_exact(ctx, layer, fn)) return rc;
     SplitBufs sb;
     const float* w_inv = nullptr;
-    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn)) return rc;
+    if (int rc = batch_gemm(ctx, layer, n_tok, xb, &sb, &w_inv, fn, exact)) return rc;
     const auto& p = ctx->proj[layer];
+    const int ld = (int)(ctx->q_dim + 2 * ctx->kv_dim);
+    if (exact)  // the k and v columns of the GEMM result, in the reference's order
+        if (int rc = exact_kv(ctx, layer, n_tok, xb, sb.y + ctx->q_dim, sb.y + ctx->q_dim + ctx->kv_dim, ld, fn))
+            return rc;
     pqa::PrefillScaled ys;
     ys.y = sb.y;
-    ys.ld = (int)(ctx->q_dim + 2 * ctx->kv_dim);
+    ys.ld = ld;
     ys.w_inv = w_inv;
     ys.x_inv = sb.x_inv;
     for (int i = 0; i < 3; i++) {
         ys.b[i] = (const uint8_t*)p.b[i];
         ys.bt[i] = p.btype[i];
     }
+    ys.kv_plain = exact;
     return hip_check(ctx, pqa::launch_prefill_scaled(ctx, layer, start_pos, n_tok, ys, out), fn);
 }
 
@@ -538,7 +590,15 @@ extern "C" int pqa_prefill_block(pqa_ctx* ctx, int layer, int start_pos, int n_t
     }
     if (int rc = ensure_layer_split(ctx, layer, fn)) return rc;
     if (int rc = ensure_layer_out_split(ctx, layer, fn)) return rc;
+    if (ctx->batch_exact_kv)
+        if (int rc = ensure_layer_exact(ctx, layer, fn)) return rc;
     if (int rc = pqa_prefill_x(ctx, layer, start_pos, n_tok, xb, ctx->battn)) return rc;
     return out_project_batch(ctx, layer, n_tok, ctx->battn, x, fn);
 }
 
+extern "C" int pqa_set_batch_projection(pqa_ctx* ctx, int exact_kv) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_batch_projection: ctx is NULL");
+    if (exact_kv != 0 && exact_kv != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_batch_projection: 0 or 1");
+    ctx->batch_exact_kv = exact_kv;
+    return PQA_OK;
+}

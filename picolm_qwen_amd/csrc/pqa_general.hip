@@ -584,7 +584,8 @@ hipError_t launch_prefill_general(pqa_ctx* ctx, int layer, int start, int n_tok,
         const size_t off[3] = {0, ctx->q_dim, ctx->q_dim + ctx->kv_dim};
         GenSrc* s[3] = {&sq, &sk, &sv};
         for (int i = 0; i < 3; i++)
-            *s[i] = GenSrc{ys->y + off[i], ys->ld, ys->w_inv + off[i], ys->x_inv, ys->b[i], ys->bt[i]};
+            *s[i] = i > 0 && ys->kv_plain ? GenSrc{ys->y + off[i], ys->ld, nullptr, nullptr, nullptr, 0}
+                                          : GenSrc{ys->y + off[i], ys->ld, ys->w_inv + off[i], ys->x_inv, ys->b[i], ys->bt[i]};
     } else {
         sq = plain_src(q, ctx->q_dim);
         sk = plain_src(k, ctx->kv_dim);

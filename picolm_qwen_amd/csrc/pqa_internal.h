@@ -29,6 +29,11 @@ struct pqa_proj_weights {
     void* split = nullptr;
     // the same for the attn_output rows (pqa_out_project_batch)
     void* out_split = nullptr;
+    // the batched path's attn_k and attn_v rows for the reference-order
+    // projection (pqa_exact.hip): fp32 [kv_dim][n_embd] each (Q8_0: the int8
+    // values as floats, then the block scales); made on the first call that
+    // needs them, dropped with the weights
+    float* exact = nullptr;
 };
 
 struct pqa_ctx {
@@ -56,6 +61,11 @@ struct pqa_ctx {
     // prefill q: 1 (default) fp16 hi + lo, fp32-level scores; 0 one fp16 q,
     // whose score error grows with |q| |k|
     int prefill_split_q = 1;
+
+    // batched projections: 1 (default) the K and V columns in the reference's
+    // summation order (bit-exact cache rows), q on the split fp16 GEMM; 0 all
+    // three on the split GEMM
+    int batch_exact_kv = 1;
 
     // projections (pqa_set_qkv_weights) and the q/k/v of pqa_decode_x
     std::vector<pqa_proj_weights> proj;
@@ -136,6 +146,8 @@ hipError_t launch_prefill(pqa_ctx* ctx, int layer, int start, int n_tok, const f
 // q/k/v of a prompt as the columns of one GEMM result y [n_tok][ld] (q at
 // column 0, k at q_dim, v at q_dim + kv_dim), scaled by powers of two: the
 // value of column c of token t is y * (w_inv[c] * x_inv[t]) + b_m[c]
+// With kv_plain, the k and v columns hold final values (the reference-order
+// projection wrote them, biases included) and are read as they are.
 struct PrefillScaled {
     const float* y;
     int ld;
@@ -143,6 +155,7 @@ struct PrefillScaled {
     const float* x_inv;
     const uint8_t* b[3];  // q, k, v biases or null
     int bt[3];
+    bool kv_plain;
 };
 hipError_t launch_prefill_scaled(pqa_ctx* ctx, int layer, int start, int n_tok, const PrefillScaled& ys, float* out);
 // The general-head_dim path (pqa_general.hip): the same contracts as
@@ -155,6 +168,17 @@ hipError_t launch_prefill_general(pqa_ctx* ctx, int layer, int start, int n_tok,
 hipError_t launch_synth_kv(pqa_ctx* ctx, int layer, int pos0, int n, uint64_t seed, float prob);
 hipError_t launch_f32_to_f16(pqa_ctx* ctx, const float* src, uint16_t* dst, size_t n);
 hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);
+// GGUF rows [rows][n] -> fp32 [rows][n] by the dequantize_row_* expressions
+// (pqa_batch.hip).
+hipError_t launch_dequant_rows(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s);
+// The reference-order projection of a prompt (pqa_exact.hip):
+// exact_matrix_floats / prepare_exact_matrix make a matrix's prepared copy
+// from its GGUF rows; launch_ordered_project writes out[t * ldo + r] =
+// matmul_bias of token t's input x[t * ldx ..] for rows r < rows, bit-exact.
+size_t exact_matrix_floats(int type, int rows, int n);
+hipError_t prepare_exact_matrix(int type, const void* w, int stride, int rows, int n, float* dst, hipStream_t s);
+hipError_t launch_ordered_project(int type, const float* prepared, int rows, int n, const float* x, int ldx, int n_tok,
+                                  const void* bias, int btype, float* out, int ldo, hipStream_t s);
 hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x);
 
 }  // namespace pqa

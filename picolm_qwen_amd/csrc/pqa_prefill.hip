@@ -715,10 +715,13 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     p.kw = p.vw = p.x_inv = nullptr;
     p.kb = p.vb = nullptr;
     p.kbt = p.vbt = 0;
-    if (YS) {
+    const bool kv_scaled = YS && !ys->kv_plain;
+    if (YS) {  // k and v are columns of the GEMM result; scaled unless the reference-order projection wrote them
         p.k = ys->y + ctx->q_dim;
         p.v = ys->y + ctx->q_dim + ctx->kv_dim;
         p.ld = ys->ld;
+    }
+    if (kv_scaled) {
         p.kw = ys->w_inv + ctx->q_dim;
         p.vw = ys->w_inv + ctx->q_dim + ctx->kv_dim;
         p.x_inv = ys->x_inv;
@@ -729,8 +732,11 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
     }
     constexpr int rows_per_wg = (kKvThreads / 64) * (64 / (HD / 4));
     const int n_items = n_tok * ctx->n_kv_heads;
-    hipLaunchKernelGGL((prefill_kv_kernel<HD, YS>), dim3((n_items + rows_per_wg - 1) / rows_per_wg), dim3(kKvThreads),
-                       0, ctx->stream, p);
+    const dim3 kv_grid((n_items + rows_per_wg - 1) / rows_per_wg);
+    if (kv_scaled)
+        hipLaunchKernelGGL((prefill_kv_kernel<HD, true>), kv_grid, dim3(kKvThreads), 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL((prefill_kv_kernel<HD, false>), kv_grid, dim3(kKvThreads), 0, ctx->stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
 

@@ -408,6 +408,8 @@ void free_proj(pqa_ctx* c, int layer) {
     p.split = nullptr;
     if (p.out_split) (void)hipFree(p.out_split);
     p.out_split = nullptr;
+    if (p.exact) (void)hipFree(p.exact);
+    p.exact = nullptr;
 }
 
 }  // namespace
@@ -476,8 +478,10 @@ extern "C" int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const vo
     if (ctx->proj.empty()) ctx->proj.resize(ctx->n_layers);
     auto& p = ctx->proj[layer];
     for (int i = 0; i < 3; i++) free_matrix(p, i);
-    if (p.split) (void)hipFree(p.split);  // the batched path's copy of the old rows
+    if (p.split) (void)hipFree(p.split);  // the batched path's copies of the old rows
     p.split = nullptr;
+    if (p.exact) (void)hipFree(p.exact);
+    p.exact = nullptr;
     p.n_embd = 0;
     for (int i = 0; i < 3; i++)
         if (int rc = upload_matrix(ctx, p, i, fn, n_embd, rows[i], w[i], wt[i], b[i], bt[i])) {

@@ -333,17 +333,36 @@ def test_batched_projection_multi_tile_and_k_padding():
     att.close()
 
 
-def test_prompt_path_from_xb_with_biases():
+def _check_prompt_rows(got_rows, want_rows, exact_kv):
+    """Appended K/V rows of the prompt path: byte-equal with the reference-order
+    K/V projection (the default); with the split GEMM a few elements may round
+    to the neighbouring fp16 value (the projection's ~1e-6 relative reordering
+    carried through norm and RoPE)."""
+    for name, g, wnt in zip("KV", got_rows, want_rows):
+        if exact_kv:
+            assert_bits_equal(g, wnt, f"{name} rows from xb")
+            continue
+        same = g == wnt
+        gf, wf = g.view(np.float16).astype(np.float64), wnt.view(np.float16).astype(np.float64)
+        slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
+        assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
+
+
+@pytest.mark.parametrize("exact_kv", [True, False])
+def test_prompt_path_from_xb_with_biases(exact_kv):
     # Qwen2.5-style layer: q/k/v biases (F32 and F16), no QK-norm, hd 64,
     # a prompt continuing at position 40; the prefill kernels read the scaled
-    # GEMM result, undo the scale and add the biases themselves. q and k here
-    # have std 2 (scores up to ~11): the default hi + lo q keeps the scores at
-    # fp32 level (one fp16 q would miss the tolerance here)
-    print("prefill_x with biases", flush=True)
+    # GEMM result, undo the scale and add the biases themselves (q always; k
+    # and v only with the split-GEMM K/V projection). q and k here have std 2
+    # (scores up to ~11): the default hi + lo q keeps the scores at fp32 level
+    # (one fp16 q would miss the tolerance here)
+    print(f"prefill_x with biases, exact_kv {exact_kv}", flush=True)
     rng = np.random.default_rng(1414)
     nh, nkv, hd, dim, n_tok, smax, start = 14, 2, 64, 896, 70, 160, 40
     cos, sin = O.rope_table(1e6, hd, smax)
     att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    if not exact_kv:
+        att.set_batch_projection(False)
     mats = [(make_rows(rng, O.GGUF_Q8_0, nh * hd, dim), make_bias(rng, O.GGUF_F32, nh * hd), O.GGUF_F32),
             (make_rows(rng, O.GGUF_Q8_0, nkv * hd, dim), make_bias(rng, O.GGUF_F16, nkv * hd), O.GGUF_F16),
             (make_rows(rng, O.GGUF_Q8_0, nkv * hd, dim), make_bias(rng, O.GGUF_F32, nkv * hd), O.GGUF_F32)]
@@ -360,24 +379,22 @@ def test_prompt_path_from_xb_with_biases():
     want = O.prefill(O.shape(nh, nkv, hd, smax, 0), start, *qkv, None, None, cos, sin, kc, vc)
     out = att.forward_batch_x(0, start, torch.from_numpy(x).to(torch.device("cuda:0"))).cpu().numpy()
     assert_close(out, want)
-    gk, gv = att.kv_download(0, start, n_tok)
-    for name, g, wnt in (("K", gk, kc[start:start + n_tok]), ("V", gv, vc[start:start + n_tok])):
-        same = g == wnt
-        gf, wf = g.view(np.float16).astype(np.float64), wnt.view(np.float16).astype(np.float64)
-        slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
-        assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
+    _check_prompt_rows(att.kv_download(0, start, n_tok), (kc[start:start + n_tok], vc[start:start + n_tok]), exact_kv)
     att.close()
 
 
-def test_prompt_path_from_xb_matches_oracle():
+@pytest.mark.parametrize("exact_kv", [True, False])
+def test_prompt_path_from_xb_matches_oracle(exact_kv):
     # pqa_prefill_x = batched projections + the MFMA prefill: outputs within the
-    # attention tolerance; K rows carry the projection's reordering, so a few
-    # elements may round to the neighbouring fp16 value
-    print("prefill_x", flush=True)
+    # attention tolerance; K/V rows byte-equal with the reference-order K/V
+    # projection, within one fp16 step (>= 99 % equal) with the split GEMM
+    print(f"prefill_x, exact_kv {exact_kv}", flush=True)
     rng = np.random.default_rng(2718)
     nh, nkv, hd, dim, n_tok, smax = 16, 8, 128, 2048, 96, 128
     cos, sin = O.rope_table(1e6, hd, smax)
     att = PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    if not exact_kv:
+        att.set_batch_projection(False)
     qn, kn = O.qk_norm_weights(9, 0, hd)
     att.set_qk_norm(0, qn, kn)
     wq = make_rows(rng, O.GGUF_Q4_K, nh * hd, dim)
@@ -393,14 +410,7 @@ def test_prompt_path_from_xb_matches_oracle():
     want = O.prefill(O.shape(nh, nkv, hd, smax, 0), 0, q, k, v, qn, kn, cos, sin, kc, vc)
     out = att.forward_batch_x(0, 0, torch.from_numpy(x).to(torch.device("cuda:0"))).cpu().numpy()
     assert_close(out, want)
-    gk, gv = att.kv_download(0, 0, n_tok)
-    for name, g, wnt in (("K", gk, kc[:n_tok]), ("V", gv, vc[:n_tok])):
-        same = g == wnt
-        gf, wf = g.view(np.float16).astype(np.float64), wnt.view(np.float16).astype(np.float64)
-        # one fp16 rounding of the value, plus the projection's reordering
-        # (1e-6 relative to the row scale) carried through norm and RoPE
-        slack = 2.0 ** -10 * np.abs(wf) + 1e-4 * np.abs(wf).max()
-        assert same.mean() >= 0.99 and np.all(np.abs(gf - wf) <= slack), (name, float(same.mean()))
+    _check_prompt_rows(att.kv_download(0, 0, n_tok), (kc[:n_tok], vc[:n_tok]), exact_kv)
     att.close()
 
 

@@ -132,3 +132,19 @@ def test_sse2_order_is_the_one_restated():
     for v in w:
         seq = np.float32(seq + v)
     assert got == want and want != seq
+
+
+@pytest.mark.parametrize("wtype", TYPES)
+def test_matmul_bias_tokens_equals_per_token_calls(wtype):
+    # the threaded batched form (the prompt-path checker) gives, for every
+    # token, the bits of the per-token matmul_bias pinned to the reference above
+    rng = np.random.default_rng(4242 + wtype)
+    rows, n, n_tok = 37, 512, 9
+    w = make_rows(rng, wtype, rows, n, special=True)
+    x = rng.standard_normal((n_tok, n)).astype(np.float32)
+    for btype in (O.GGUF_NONE, O.GGUF_F32, O.GGUF_F16):
+        b = None if btype == O.GGUF_NONE else make_bias(rng, btype, rows)
+        for threads in (1, 4):
+            got = O.matmul_bias_tokens(x, w, wtype, rows, b, btype, n_threads=threads)
+            for t in range(n_tok):
+                assert bits_equal(got[t], O.matmul_bias(x[t], w, wtype, rows, b, btype)), (wtype, btype, threads, t)
