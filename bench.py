@@ -665,13 +665,20 @@ def prefill_x_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, dim=2560, 
 COPY_BYTES = 1 << 30  # the calibration copy: reads and writes 1 GiB
 
 
-def pmc_probe(torch, dev):
-    """The dispatches the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)
-    count: the headline decode (36 layers x 2 steps, same cache and inputs as
-    the bench) and three launches of a plain elementwise copy of known size
-    (torch.neg over 1 GiB of fp32: 1 GiB read + 1 GiB written), whose counter
-    readings give the bytes-per-count scale."""
-    decode_workload(torch, dev, "qwen3_8b_decode", 36, 32, 8, 128, 0, 1e6, 131071, 0.01, 2, 0, True)
+# the decode shapes a --pmc-probe can run: (workload name, n_layers, nh, nkv, hd, pos, outlier prob)
+PMC_SHAPES = {"c5": ("qwen3_8b_decode", 36, 32, 8, 128, 131071, 0.01),
+              "c3": ("qwen3_1.7b_decode", 28, 16, 8, 128, 32767, 0.0)}
+
+
+def pmc_probe(torch, dev, which="c5"):
+    """The dispatches the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, or
+    other counters) count: a decode workload (C5, the headline: 36 layers x 2
+    steps; or C3: 28 layers x 2 steps; same caches and inputs as the bench) and
+    three launches of a plain elementwise copy of known size (torch.neg over 1
+    GiB of fp32: 1 GiB read + 1 GiB written), whose counter readings give the
+    bytes-per-count scale."""
+    name, nl, nh, nkv, hd, pos, prob = PMC_SHAPES[which]
+    decode_workload(torch, dev, name, nl, nh, nkv, hd, 0, 1e6, pos, prob, 2, 0, True)
     src = torch.ones(COPY_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -694,9 +701,12 @@ def _find(d, suffix):
     raise FileNotFoundError(f"no *{suffix} under {d}")
 
 
-def summarize_pmc(fetch_dir, write_dir):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the headline decode
-    kernels, scaled by the calibration copy's bytes per KiB counted."""
+def summarize_pmc(fetch_dir, write_dir, which="c5"):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the decode kernels of a
+    --pmc-probe run (C5: query-head chunk 4; C3: 2), scaled by the calibration
+    copy's bytes per KiB counted."""
+    _, _, nh, nkv, hd, pos, _ = PMC_SHAPES[which]
+    chunk = min(nh // nkv, 8)
     out = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         groups = {}
@@ -704,8 +714,9 @@ def summarize_pmc(fetch_dir, write_dir):
             if r.get("Counter_Name") != counter:
                 continue
             name = r["Kernel_Name"]
-            key = ("copy" if "neg_kernel" in name else "decode" if re.search(r"decode_kernel<128, 4[,>]", name)
-                   else "combine" if "decode_combine_kernel<128>" in name else None)
+            key = ("copy" if "neg_kernel" in name else
+                   "decode" if re.search(rf"decode_kernel<{hd}, {chunk}[,>]", name)
+                   else "combine" if re.search(rf"decode_combine(_wave)?_kernel<{hd}>", name) else None)
             if key:
                 groups.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
                 groups[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
@@ -721,7 +732,7 @@ def summarize_pmc(fetch_dir, write_dir):
         wk, _ = out["WRITE_SIZE"][k]
         res[k] = (fk * f_scale, wk * w_scale)
         lines.append(f"{k:36s}{nf:10d}  {fk:14.1f}  {wk:14.1f}  {fk * f_scale:13.0f}  {wk * w_scale:13.0f}")
-    alg = decode_bytes(131072, 32, 8, 128)
+    alg = decode_bytes(pos + 1, nh, nkv, hd)
     traffic = res["decode"][0] + res["decode"][1] + res["combine"][0] + res["combine"][1]
     lines += ["",
               f"scale: reads {f_scale:.1f} B per FETCH_SIZE KiB, writes {w_scale:.1f} B per WRITE_SIZE KiB "
@@ -1006,7 +1017,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
-    ap.add_argument("--pmc-probe", action="store_true", help="dispatches for the rocprofv3 --pmc passes")
+    ap.add_argument("--pmc-probe", nargs="?", const="c5", choices=sorted(PMC_SHAPES),
+                    help="dispatches for the rocprofv3 --pmc passes (c5, the default, or c3)")
+    ap.add_argument("--pmc-shape", default="c5", choices=sorted(PMC_SHAPES), help="decode shape of --summarize-pmc")
     ap.add_argument("--only", choices=["qwen3_1.7b_decode", "qwen3_4b_prefill", "tinyllama_decode",
                                        "qwen2.5_0.5b_sweep", "qwen3_8b_kvc_save_load", "qwen3_8b_qkv_proj",
                                        "qwen3_4b_prefill_from_xb"],
@@ -1032,7 +1045,7 @@ def main():
         print(summarize_counters(args.summarize_counters, args.kernel))
         return
     if args.summarize_pmc:
-        print(summarize_pmc(*args.summarize_pmc))
+        print(summarize_pmc(*args.summarize_pmc, which=args.pmc_shape))
         return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
@@ -1047,7 +1060,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     if args.pmc_probe:
-        pmc_probe(torch, dev)
+        pmc_probe(torch, dev, args.pmc_probe)
         return
     cpu_on = not args.no_cpu
     runs = secondary_workloads(torch, dev, args.steps, args.warmup, cpu_on)

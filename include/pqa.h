@@ -94,18 +94,21 @@ int pqa_prefill(pqa_ctx* ctx, int layer, int start_pos, int n_tok, const float* 
                 const float* v, float* out);
 
 /*
- * pqa_decode that allocates nothing and uses no context workspace: the same
- * kernels, with the split partials in a static device array of the library
- * (8 MiB per GPU, held until the process ends; its address is taken once per
- * device by pqa_create). No counterpart in the reference: this entry point is
- * for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * arguments, results and errors as pqa_decode, plus PQA_ERR_UNSUPPORTED when
- * two splits' partials of the context's head count exceed the 8 MiB
- * (n_kv_heads * ceil(g / 8) * chunk heads * (head_dim + 2) * 8 bytes; about
- * 8000 query heads); the split count is capped at what fits. Every call on
- * one GPU shares the array: calls that overlap on one GPU (other streams or
- * threads) race and must be ordered by the caller.
+ * pqa_decode that allocates nothing: the same kernels, with the split
+ * partials in a static device array of the library (8 MiB per GPU, held until
+ * the process ends; its address is taken once per device by pqa_create)
+ * instead of the context's split workspace. Head sizes other than 64 and 128
+ * also use the prepared-q buffer that pqa_create allocates (one token's q,
+ * read and written, never grown by this call). No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, results and errors as pqa_decode. The
+ * split count is capped at what fits in the 8 MiB (each split's partials take
+ * n_kv_heads * ceil(g / 8) * chunk heads * (head_dim + 2) * 4 bytes); when
+ * not even two fit (about 8000 query heads), every call runs as one split,
+ * which needs no scratch. Every call on one GPU shares the array: calls that
+ * overlap on one GPU (other streams or threads) race and must be ordered by
+ * the caller.
  */
 int pqa_decode_noalloc(pqa_ctx* ctx, int layer, int pos, const float* q, const float* k, const float* v,
                        float* out);

@@ -232,6 +232,13 @@ static int ensure_stage(pqa_ctx* ctx, size_t floats) {
 // where the runtime pipelines its own staging.
 constexpr size_t kHostStageBytes = size_t(4) << 20;
 
+// The pinned staging buffer of the host entries: hipHostMallocDefault, i.e.
+// mapped host memory whose coherence kind follows HIP_HOST_COHERENT (fine-
+// grained when it is set, coarse-grained otherwise). Either kind is correct
+// here because every use is bracketed the same way: the CPU writes the inputs
+// before the launch that reads them (a kernel start acquires at system scope)
+// and reads the outputs only after hipStreamSynchronize (a kernel end
+// releases at system scope); no kernel and CPU touch the buffer at once.
 static int ensure_hstage(pqa_ctx* ctx, size_t floats) {
     if (floats <= ctx->hstage_floats) return PQA_OK;
     if (ctx->hstage) (void)hipHostFree(ctx->hstage);

@@ -875,16 +875,14 @@ int scratch_workspace(pqa_ctx* ctx, DecodeWorkspace* ws, const char* fn) {
     }
     if (!base) return set_err(ctx, PQA_ERR_HIP, std::string(fn) + ": no scratch address for this device");
     // As many splits as fit: each takes ny * G * (hd + 2) floats. Fewer splits
-    // than pqa_decode may use only lengthen each split's row range.
+    // than pqa_decode may use only lengthen each split's row range; when not
+    // even two splits' partials fit, every call runs as one split, which
+    // writes the output directly and needs no scratch (slow for long
+    // histories, but never refused).
     const size_t ny = (size_t)ctx->n_kv_heads * ctx->n_chunk;
     const size_t per_split = ny * ctx->chunk_heads * (ctx->head_dim + 2);
     const size_t fit = kScratchBytes / sizeof(float) / per_split;
-    if (fit < 2)
-        return set_err(ctx, PQA_ERR_UNSUPPORTED,
-                       std::string(fn) + ": the split partials of this head count need " +
-                           std::to_string(2 * per_split * sizeof(float)) + " bytes, above the " +
-                           std::to_string(kScratchBytes) + "-byte scratch");
-    ws->max_splits = (int)std::min<size_t>(fit, (size_t)ctx->max_splits);
+    ws->max_splits = fit < 2 ? 1 : (int)std::min<size_t>(fit, (size_t)ctx->max_splits);
     ws->part_acc = base;
     ws->part_ml = base + ny * ws->max_splits * ctx->chunk_heads * ctx->head_dim;
     return PQA_OK;

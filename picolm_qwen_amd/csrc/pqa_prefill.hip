@@ -1,9 +1,9 @@
 // Causal prefill of one layer: the token loop of cpp/model.hpp:493-593 as two
 // launches.
 //
-// 1. prefill_kv: the new cache rows. One wave per 64/(HD/4) (token, KV head)
-//    rows: K gets the QK-RMSNorm in the reference's summation order, RoPE at
-//    the token's position and the reference's fp16 rounding; V the rounding
+// 1. prefill_kv: the new cache rows. One wave per 2 (token, KV head) rows:
+//    K gets the QK-RMSNorm in the reference's summation order, RoPE at the
+//    token's position and the reference's fp16 rounding; V the rounding
 //    only. Rows start..start+n-1 of the layer slice are written.
 // 2. prefill_attn: flash attention over the fp16 cache on
 //    v_mfma_f32_32x32x16_f16. The query heads of one KV head are packed as
@@ -66,54 +66,93 @@ __device__ __forceinline__ float4 unscale4(float4 y, float4 w, float xi, const u
 }
 
 constexpr int kKvThreads = 256;
+// (token, KV head) rows per wave, at least one row per 16 lanes' float4s.
+// Measured at Qwen3-4B shape (16384 rows): 2 -> 7.46 us, 4 -> 8.08, 8 -> 8.82,
+// 16 -> 10.4 (fewer, fuller waves hide the load round trip worse).
+#ifndef PQA_KV_ROWS_PER_WAVE
+#define PQA_KV_ROWS_PER_WAVE 2
+#endif
+constexpr int kKvRowsPerWave = PQA_KV_ROWS_PER_WAVE;
+
+// RPW rows per wave. Each lane holds NS float4s of K and of V: slot i, lane l
+// -> row RPS i + l / H4 of the wave's RPW, elements 4 (l % H4) .. +3 (RPS =
+// 64 / H4 rows per slot). All loads (K, V, the RoPE rows) are issued first.
+// The K RMSNorm runs in the reference's order: the rows go to LDS, lane
+// (r, j) = (l / 4, l % 4) sums SSE lane j of row r (rms_scale_ref_quad), and
+// each lane reads back the scales of its slots' rows. RoPE partners come over
+// lanes (rope_lanes), then the reference's fp16 rounding and 8-byte stores.
+template <int HD>
+constexpr int kv_rows_per_wave() { return kKvRowsPerWave < 256 / HD ? 256 / HD : kKvRowsPerWave; }
 
 template <int HD, bool YS>
 __global__ __launch_bounds__(kKvThreads) void prefill_kv_kernel(const KvArgs a) {
-    constexpr int H4 = HD / 4;
-    constexpr int IPW = 64 / H4;  // rows per wave
+    constexpr int H4 = HD / 4;        // lanes per row
+    constexpr int RPS = 64 / H4;      // rows per slot
+    constexpr int RPW = kv_rows_per_wave<HD>();
+    static_assert(RPW % RPS == 0 && RPW <= 16, "whole slots, at most 4 lanes per row for the norm chains");
+    constexpr int NS = RPW / RPS;     // slots per lane
     constexpr int NW = kKvThreads / 64;
-    __shared__ __attribute__((aligned(16))) float sk[NW][IPW][HD];
-    __shared__ float s_scale[NW][IPW];
+    constexpr int RS = HD + 4;        // LDS row stride in floats (rows r and r + 8 share banks: 2-way)
+    __shared__ __attribute__((aligned(16))) float sk[NW][RPW * RS];
+    __shared__ float s_scale[NW][RPW];
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int w = threadIdx.x >> 6;
     const int t = lane % H4, hh = lane / H4;
     const int n_items = a.n_tok * a.nkv;
-    const int item = (blockIdx.x * NW + w) * IPW + hh;
-    const int it = min(item, n_items - 1);  // loads stay in bounds; stores are predicated
-    const int tok = it / a.nkv, kvh = it - tok * a.nkv;
-    const int pos = a.start + tok;
+    const int item0 = (blockIdx.x * NW + w) * RPW;
     const size_t kv_dim = (size_t)a.nkv * HD;
-    float4 kx = ((const float4*)(a.k + (size_t)tok * a.ld + (size_t)kvh * HD))[t];
-    float4 vx = ((const float4*)(a.v + (size_t)tok * a.ld + (size_t)kvh * HD))[t];
-    if constexpr (YS) {
-        const float xi = a.x_inv[tok];
-        const int c = kvh * HD + 4 * t;
-        kx = unscale4(kx, ((const float4*)(a.kw + (size_t)kvh * HD))[t], xi, a.kb, a.kbt, c);
-        vx = unscale4(vx, ((const float4*)(a.vw + (size_t)kvh * HD))[t], xi, a.vb, a.vbt, c);
+    const int ci = rope_angle_f4<HD>(a.rope, t);
+
+    float4 kx[NS], vx[NS], cs[NS], sn[NS];
+    int tok[NS], kvh[NS];
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const int it = min(item0 + RPS * i + hh, n_items - 1);  // loads stay in bounds; stores are predicated
+        tok[i] = it / a.nkv;
+        kvh[i] = it - tok[i] * a.nkv;
+        const size_t off = (size_t)tok[i] * a.ld + (size_t)kvh[i] * HD;
+        kx[i] = ((const float4*)(a.k + off))[t];
+        vx[i] = ((const float4*)(a.v + off))[t];
+        const size_t pos = (size_t)(a.start + tok[i]);
+        cs[i] = ((const float4*)(a.cos_tab + pos * (HD / 2)))[ci];
+        sn[i] = ((const float4*)(a.sin_tab + pos * (HD / 2)))[ci];
     }
     const float4 wk = ((const float4*)(a.kn ? a.kn : a.wpad + HD))[t];
-    const int ci = rope_angle_f4<HD>(a.rope, t);
-    const float4 cs = ((const float4*)(a.cos_tab + (size_t)pos * (HD / 2)))[ci];
-    const float4 sn = ((const float4*)(a.sin_tab + (size_t)pos * (HD / 2)))[ci];
-    float4 x = kx;
-    if (a.kn) {
-        ((float4*)sk[w][hh])[t] = kx;
-        wave_sync();
-        const int qd = min(lane >> 2, IPW - 1);  // quad qd sums row qd in the reference's order
-        const float s = rms_scale_ref_quad<HD>(sk[w][qd], lane & 3);
-        if ((lane & 3) == 0 && (lane >> 2) < IPW) s_scale[w][qd] = s;
-        wave_sync();
-        const float sc = s_scale[w][hh];
-        x = float4{rms_apply(x.x, sc, wk.x), rms_apply(x.y, sc, wk.y), rms_apply(x.z, sc, wk.z),
-                   rms_apply(x.w, sc, wk.w)};
+    if constexpr (YS) {
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const float xi = a.x_inv[tok[i]];
+            const int c = kvh[i] * HD + 4 * t;
+            kx[i] = unscale4(kx[i], ((const float4*)(a.kw + (size_t)kvh[i] * HD))[t], xi, a.kb, a.kbt, c);
+            vx[i] = unscale4(vx[i], ((const float4*)(a.vw + (size_t)kvh[i] * HD))[t], xi, a.vb, a.vbt, c);
+        }
     }
-    x = rope_lanes<HD>(x, a.rope, t, cs, sn);
-    if (item < n_items) {
-        const size_t off = (size_t)pos * kv_dim + (size_t)kvh * HD + 4 * t;
-        *(u32x2*)(a.kc + off) = u32x2{f32_to_f16_ref(x.x) | ((uint32_t)f32_to_f16_ref(x.y) << 16),
-                                      f32_to_f16_ref(x.z) | ((uint32_t)f32_to_f16_ref(x.w) << 16)};
-        *(u32x2*)(a.vc + off) = u32x2{f32_to_f16_ref(vx.x) | ((uint32_t)f32_to_f16_ref(vx.y) << 16),
-                                      f32_to_f16_ref(vx.z) | ((uint32_t)f32_to_f16_ref(vx.w) << 16)};
+    if (a.kn) {
+        float* rows = sk[w];
+#pragma unroll
+        for (int i = 0; i < NS; i++) ((float4*)(rows + (RPS * i + hh) * RS))[t] = kx[i];
+        wave_sync();
+        const int r = min(lane >> 2, RPW - 1);  // lane (r, j): SSE lane j of row r
+        const float s = rms_scale_ref_quad<HD>(rows + r * RS, lane & 3);
+        if ((lane & 3) == 0 && (lane >> 2) < RPW) s_scale[w][r] = s;
+        wave_sync();
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const float sc = s_scale[w][RPS * i + hh];
+            kx[i] = float4{rms_apply(kx[i].x, sc, wk.x), rms_apply(kx[i].y, sc, wk.y), rms_apply(kx[i].z, sc, wk.z),
+                           rms_apply(kx[i].w, sc, wk.w)};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const float4 x = rope_lanes<HD>(kx[i], a.rope, t, cs[i], sn[i]);
+        if (item0 + RPS * i + hh < n_items) {
+            const size_t off = (size_t)(a.start + tok[i]) * kv_dim + (size_t)kvh[i] * HD + 4 * t;
+            *(u32x2*)(a.kc + off) = u32x2{f32_to_f16_ref(x.x) | ((uint32_t)f32_to_f16_ref(x.y) << 16),
+                                          f32_to_f16_ref(x.z) | ((uint32_t)f32_to_f16_ref(x.w) << 16)};
+            *(u32x2*)(a.vc + off) = u32x2{f32_to_f16_ref(vx[i].x) | ((uint32_t)f32_to_f16_ref(vx[i].y) << 16),
+                                          f32_to_f16_ref(vx[i].z) | ((uint32_t)f32_to_f16_ref(vx[i].w) << 16)};
+        }
     }
 }
 
@@ -730,7 +769,7 @@ static hipError_t launch_prefill_hd(pqa_ctx* ctx, int layer, int start, int n_to
         p.vb = ys->b[2];
         p.vbt = ys->bt[2];
     }
-    constexpr int rows_per_wg = (kKvThreads / 64) * (64 / (HD / 4));
+    constexpr int rows_per_wg = (kKvThreads / 64) * kv_rows_per_wave<HD>();
     const int n_items = n_tok * ctx->n_kv_heads;
     const dim3 kv_grid((n_items + rows_per_wg - 1) / rows_per_wg);
     if (kv_scaled)

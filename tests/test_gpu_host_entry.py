@@ -66,3 +66,30 @@ def test_decode_host_successive_calls_and_a_failed_call():
     assert np.array_equal(kh, kd) and np.array_equal(vh, vd)
     host.close()
     dev.close()
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos", [
+    (16, 8, 128, 8191),    # whole-row workgroups, several splits: the merge launch writes out into host memory
+    (16, 8, 128, 32767),   # Qwen3-1.7B shape at its full context
+    (32, 4, 64, 2047),     # hd 64, several splits
+    (8, 2, 96, 3000),      # a general head size (VALU kernels, their own merge)
+])
+def test_decode_host_multi_split_and_general_equal_device_entry(nh, nkv, hd, pos):
+    # the zero-copy host entry (kernels read q/k/v from and write out into the
+    # pinned staging buffer) against the device entry at launch shapes the
+    # single-split cases above do not reach: bit-equal outputs and rows
+    print(f"decode host entry {nh}/{nkv}/{hd} pos {pos}", flush=True)
+    seed = 7400 + pos
+    host, dev = _pair(nh, nkv, hd, pos + 1, seed)
+    for att in (host, dev):
+        att.synth_kv(0, 0, pos, seed, 0.01)
+    q, k, v = O.step_inputs(seed, 0, pos, nh, nkv, hd)
+    got = host.forward(0, pos, q, k, v)
+    want = dev.forward(0, pos, _device(q), _device(k), _device(v))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want.cpu().numpy())
+    kh, vh = host.kv_download(0, pos, 1)
+    kd, vd = dev.kv_download(0, pos, 1)
+    assert np.array_equal(kh, kd) and np.array_equal(vh, vd)
+    host.close()
+    dev.close()

@@ -82,17 +82,26 @@ def test_noalloc_other_shape_on_the_same_gpu():
     _case(14, 2, 64, 4096, 0, 1e6, False, [4095, 1000, 3], seed=8802)
 
 
-def test_noalloc_rejects_heads_whose_partials_exceed_the_scratch():
-    # 8192 KV heads x 1 query head x (128 + 2) floats x 2 splits = 8.5 MB > 8 MiB;
-    # refused before any kernel is launched
+def test_noalloc_runs_one_split_when_partials_exceed_the_scratch():
+    # 8192 KV heads x 1 query head x (128 + 2) floats x 2 splits = 8.5 MB > 8 MiB:
+    # the call runs as one split (no scratch) instead of being refused, and
+    # equals pqa_decode bit for bit (which at this head count takes one split
+    # too), at a per-column launch (pos 1) and a whole-row launch (pos 600)
     nh = nkv = 8192
-    hd, smax = 128, 2
+    hd, smax = 128, 601
     att = PicoAttention(1, smax, nh, nkv, hd, 0)
+    att.synth_kv(0, 0, smax - 1, 8803, 0.0)
     dev = torch.device("cuda:0")
-    q = torch.zeros(nh * hd, device=dev)
-    kv = torch.zeros(nkv * hd, device=dev)
-    out = torch.zeros(nh * hd, device=dev)
-    rc = _lib.lib().pqa_decode_noalloc(att.handle, 0, 1, _ptr(q), _ptr(kv), _ptr(kv), _ptr(out))
-    assert rc == _lib.PQA_ERR_UNSUPPORTED
-    assert "scratch" in att.last_error()
+    L = _lib.lib()
+    for pos in (1, 600):
+        print(f"noalloc one split, pos {pos}", flush=True)
+        q, k, v = (torch.from_numpy(x).to(dev) for x in O.step_inputs(8803, 0, pos, nh, nkv, hd))
+        outs = []
+        for fn in (L.pqa_decode, L.pqa_decode_noalloc):
+            out = torch.zeros(nh * hd, device=dev)
+            rc = fn(att.handle, 0, pos, _ptr(q), _ptr(k), _ptr(v), _ptr(out))
+            assert rc == _lib.PQA_OK, att.last_error()
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+        assert_bits_equal(outs[1].view(np.uint32), outs[0].view(np.uint32), f"noalloc vs decode at pos {pos}")
     att.close()
