@@ -36,6 +36,7 @@ import ctypes as C
 import json
 import re
 import os
+import subprocess
 import sys
 import time
 
@@ -148,7 +149,7 @@ def median_time(fn, runs):
     return float(np.median(ts))
 
 
-def cpu_decode(cx, inputs, norms, style, base, pos, time_layers, check_layers, runs_1, runs_t):
+def cpu_decode(cx, inputs, norms, style, base, pos, time_layers, check_layers, runs_1, runs_t, ref=None):
     """The oracle's decode step (the reference's attention block,
     cpp/model.hpp:326-418, restated) on this run's own cache bytes and inputs.
 
@@ -195,7 +196,90 @@ def cpu_decode(cx, inputs, norms, style, base, pos, time_layers, check_layers, r
                      f"thread and {runs_t} on {nt} threads (query heads split) per layer, mean over layers"}
     log(f"[bench]   cpu oracle: 1 thread {us1:.1f} us/layer, {nt} threads {ust:.1f} us/layer; "
         f"layers {sorted(check_layers)} max abs err {err:.2e}, appended rows bit-exact {exact}")
+    if ref is not None:
+        # the reference's own attention beside the port, on layer 0 (ref = (seed, outlier prob, runs))
+        q, k, v, got = inputs(0)
+        r = ref_attention_cpu(cx, style, base, pos, ref[1], ref[0], q, k, v, norms, got, ref[2])
+        if r is not None:
+            if "us_per_layer_attention" in r:
+                r["port_us_per_layer_1_thread_layer0"] = round(t1[0] * 1e6, 1) if t1 else None
+            res["reference_attention"] = r
+            log(f"[bench]   reference attention (libref_A.so, 1 thread): {r}")
     return res
+
+
+def ref_attention_cpu(cx, style, base, pos, prob, seed, q, k, v, norms, gpu_out, runs):
+    """The reference's own decode step, timed: Model::forward (cpp/model.hpp:311-451)
+    built with its shipped flags (oracle/_ref/libref_A.so: -O3 -march=native,
+    GCC's default FMA contraction), one token at `pos` over the layer-0 history of
+    this run (the same seeded rows the GPU holds, regenerated on the host) on one
+    thread (its matmul pool is left at one thread; its attention loop has one).
+    The harness's one-layer model has zero-weight F32 projections, so the same
+    call at pos 0 (one history row) times everything but the attention loop; the
+    difference is the reference's attention. Run in a child process: the build
+    targets the container's CPU, and a host without one of its instructions must
+    not take the bench down. Returns a dict, or None where the build is absent."""
+    import tempfile
+    import oracle as O
+    if not O.RefModel.available("A"):
+        return None
+    fd, path = tempfile.mkstemp(suffix=".npz")
+    os.close(fd)
+    qn, kn = norms[0] if norms else (np.zeros(0, np.float32), np.zeros(0, np.float32))
+    np.savez(path, q=q, k=k, v=v, qn=qn, kn=kn, gpu_out=gpu_out,
+             shape=np.array([cx.nh, cx.nkv, cx.hd, pos, style, runs, seed], np.int64),
+             fl=np.array([base, prob], np.float64))
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--ref-attn-child", path],
+                           capture_output=True, text=True, timeout=600)
+        line = [x for x in r.stdout.splitlines() if x.startswith("{")]
+        if r.returncode != 0 or not line:
+            return {"kind": "reference", "error": f"child exited {r.returncode}: {r.stderr[-300:]}"}
+        return json.loads(line[-1])
+    finally:
+        os.unlink(path)
+
+
+def ref_attention_child(path):
+    """Body of ref_attention_cpu's child process (bench.py --ref-attn-child NPZ)."""
+    import oracle as O
+    d = np.load(path)
+    nh, nkv, hd, pos, style, runs, seed = (int(x) for x in d["shape"])
+    base, prob = (float(x) for x in d["fl"])
+    qk = d["qn"].size > 0
+    kv_dim = nkv * hd
+    t0 = time.perf_counter()
+    R = O.RefModel(nh, nkv, hd, pos + 1, base, style == 0, qk, variant="A")
+    if qk:
+        R.set_qk_norm(d["qn"], d["kn"])
+    kc, vc = O.synth_kv_rows(seed, 0, kv_dim, 0, pos, prob, cpu_threads())
+    R.set_cache_rows(0, kc, vc)
+    del kc, vc
+    setup = time.perf_counter() - t0
+    times, out = [], None
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = R.step(pos, d["q"], d["k"], d["v"])
+        times.append(time.perf_counter() - t0)
+    t_pos = float(np.median(times))
+    t0 = time.perf_counter()
+    R.step(0, d["q"], d["k"], d["v"])  # one history row: the layer without the attention loop
+    t_zero = time.perf_counter() - t0
+    R.close()
+    err = float(np.abs(out - d["gpu_out"]).max())
+    nbytes = decode_bytes(pos + 1, nh, nkv, hd)
+    print(json.dumps({
+        "kind": "reference", "cores": 1, "build": "oracle/_ref/libref_A.so (cpp/Makefile flags: -O3 -std=c++17 "
+                                                  "-march=native, built in the build container)",
+        "us_per_layer_forward": round(t_pos * 1e6, 1), "us_pos0_forward": round(t_zero * 1e6, 1),
+        "us_per_layer_attention": round((t_pos - t_zero) * 1e6, 1),
+        "non_attention_share": round(t_zero / t_pos, 4),
+        "GB_per_s_attention": round(nbytes / ((t_pos - t_zero) * 1e6) / 1e3, 3),
+        "gpu_vs_reference_max_abs_err": err, "runs": runs, "setup_s": round(setup, 1),
+        "sample": f"Model::forward of the reference's one-layer harness (zero-weight F32 projections, identity "
+                  f"attn_output) for one token at pos {pos} over the layer-0 history of this run, median of "
+                  f"{runs} run(s) on 1 thread, minus the same call at pos 0 (projections and the rest of the "
+                  f"layer)"}), flush=True)
 
 
 def host_entry_decode(cx, q, k, v, out, pos, steps):
@@ -246,7 +330,8 @@ def timed(torch, cx, fn, steps, warmup):
 
 def decode_workload(torch, dev, name, n_layers, nh, nkv, hd, style, base, pos, prob, steps, warmup, qk_norm,
                     seed=20251201, keep=False, cpu=None, host_entry=False):
-    """cpu: None, or (time_layers, check_layers, runs_1, runs_t) for cpu_decode."""
+    """cpu: None, or (time_layers, check_layers, runs_1, runs_t[, reference runs]) for cpu_decode; with a
+    fifth element the reference's own attention (libref_A.so) is timed beside the port on layer 0."""
     cx = Ctx(n_layers, pos + 1, nh, nkv, hd, style, base)
     rng = np.random.default_rng(seed)
     norms = set_norms(cx, rng, hd) if qk_norm else None
@@ -279,7 +364,8 @@ def decode_workload(torch, dev, name, n_layers, nh, nkv, hd, style, base, pos, p
     if cpu is not None:
         def inputs(layer):
             return tuple(t[layer, 0].cpu().numpy() for t in (q, k, v, out))
-        res["cpu_baseline"] = cpu_decode(cx, inputs, norms, style, base, pos, *cpu)
+        ref = (seed, prob, cpu[4]) if len(cpu) > 4 else None  # cpu[4]: reference runs at layer 0
+        res["cpu_baseline"] = cpu_decode(cx, inputs, norms, style, base, pos, *cpu[:4], ref=ref)
     if keep:
         return res, cx, (q, k, v, out)
     cx.close()
@@ -431,6 +517,7 @@ def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096,
     log(f"[bench] qwen2.5 sweep: avg {avg_us:.2f} us/layer over ctx 1..{positions}; curve {curve}")
     res = {"workload": "qwen2.5_0.5b_sweep", "n_layers": n_layers, "positions": positions,
            "avg_us_per_layer_launch_loop": round(avg_us, 3), "us_per_layer_vs_ctx": curve}
+    res.update(sweep_graphs(torch, cx, n_layers, positions, checkpoints, (qp, kp, vp, op), (qs, kvs), out))
     if cpu:
         # the oracle at two points of the curve, all layers, each layer's own inputs at that position
         res["cpu_baseline"] = {}
@@ -443,6 +530,63 @@ def sweep_workload(torch, dev, n_layers=24, nh=14, nkv=2, hd=64, positions=4096,
                                                            range(n_layers), 5, 5)
     cx.close()
     return res
+
+
+def sweep_graphs(torch, cx, n_layers, positions, checkpoints, ptrs, sizes, out):
+    """The same sweep with each position's 24-layer decode step captured once
+    into a HIP graph (pqa_decode_noalloc: no allocation, no memset; captured on
+    the library stream, picolm_qwen_amd.hipgraph) and replayed: the device-side
+    cost of a step without the host's per-launch cost. Captures every position
+    first, then replays positions 0..4095 in order (each replay re-appends the
+    row the launch loop appended, same bits), then each checkpoint's graph 20
+    times. The outputs of every replayed position are compared with the launch
+    loop's bit for bit."""
+    from picolm_qwen_amd.hipgraph import Graph
+    qp, kp, vp, op = ptrs
+    qs, kvs = sizes
+    nod, h = cx.L.pqa_decode_noalloc, cx.h
+    torch.cuda.synchronize()
+    eager = out.clone()
+
+    def step(pos):
+        for layer in range(n_layers):
+            o = (layer * positions) + pos
+            cx.check(nod(h, layer, pos, C.c_void_p(qp + o * qs), C.c_void_p(kp + o * kvs), C.c_void_p(vp + o * kvs),
+                         C.c_void_p(op + o * qs)), h)
+
+    t0 = time.perf_counter()
+    graphs = [Graph(cx.stream(), lambda pos=pos: step(pos)) for pos in range(positions)]
+    capture_s = time.perf_counter() - t0
+    ext = torch.cuda.ExternalStream(cx.stream())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out.zero_()
+    torch.cuda.synchronize()
+    e0.record(ext)
+    for g in graphs:
+        g.launch(cx.stream())
+    e1.record(ext)
+    cx.check(cx.L.pqa_sync(cx.h), cx.h)
+    torch.cuda.synchronize()
+    avg = e0.elapsed_time(e1) * 1e3 / (positions * n_layers)
+    same = bool(torch.equal(out.view(torch.int32), eager.view(torch.int32)))
+    curve = {}
+    for ctx_len in checkpoints:
+        g = graphs[ctx_len - 1]
+
+        def replay(g=g):
+            g.launch(cx.stream())
+
+        _, ev = timed(torch, cx, replay, 20, 2)
+        curve[str(ctx_len)] = round(ev * 1e3 / n_layers, 3)
+    same = same and bool(torch.equal(out.view(torch.int32), eager.view(torch.int32)))
+    for g in graphs:
+        g.close()
+    log(f"[bench] qwen2.5 sweep, graph replay: avg {avg:.2f} us/layer over ctx 1..{positions}; curve {curve}; "
+        f"equal to the launch loop {same}; {positions} captures in {capture_s:.1f} s")
+    return {"avg_us_per_layer_graph": round(avg, 3), "us_per_layer_vs_ctx_graph": curve,
+            "graph_outputs_equal_launch_loop": same,
+            "graph": "one HIP graph per position (24 layers of pqa_decode_noalloc, captured on the library stream), "
+                     "replayed in position order; the curve replays each checkpoint's graph 20 times"}
 
 
 def kvc_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n_pos=4096, reps=3):
@@ -836,7 +980,7 @@ def secondary_workloads(torch, dev, steps, warmup, cpu_on):
         # C3: every layer timed on 1 thread once and T threads 3x, every layer checked
         "qwen3_1.7b_decode": lambda: decode_workload(
             torch, dev, "qwen3_1.7b_decode", 28, 16, 8, 128, 0, 1e6, 32767, 0.0, steps, warmup, True,
-            cpu=(range(28), range(28), 1, 3) if cpu_on else None, host_entry=True)[0],
+            cpu=(range(28), range(28), 1, 3, 3) if cpu_on else None, host_entry=True)[0],
         "qwen3_4b_prefill": lambda: prefill_workload(torch, dev, 36, 32, 8, 128, 2048, max(3, steps // 5), 1,
                                                      cpu=cpu_on, host_entry=True),
         "tinyllama_decode": lambda: decode_workload(
@@ -1031,6 +1175,7 @@ def main():
     ap.add_argument("--kernel", default="prefill_attn_kernel")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-phase decode and prefill timings from the stamped build (libpqa_stamps.so)")
+    ap.add_argument("--ref-attn-child", metavar="NPZ", help=argparse.SUPPRESS)
     ap.add_argument("--sdpa-compare", action="store_true",
                     help="torch scaled_dot_product_attention on the Qwen3-4B prefill shape, for comparison")
     args = ap.parse_args()
@@ -1040,6 +1185,9 @@ def main():
     if args.phase_stamps:
         print(phase_stamps(), flush=True)
         print(prefill_phase_stamps(), flush=True)
+        return
+    if args.ref_attn_child:
+        ref_attention_child(args.ref_attn_child)
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.kernel))
@@ -1073,7 +1221,7 @@ def main():
     log(f"[bench] host CPU: {host}")
     # C5: 1 thread on layer 0 once, T threads 3x; layers 0, 17 and 35 checked (35's slice starts past 4 GiB)
     head = decode_workload(torch, dev, "qwen3_8b_decode", layers, nh, nkv, hd, 0, 1e6, pos, 0.01,
-                           args.steps, args.warmup, True, cpu=((0,), (0, 17, 35), 1, 3) if cpu_on else None,
+                           args.steps, args.warmup, True, cpu=((0,), (0, 17, 35), 1, 3, 1) if cpu_on else None,
                            host_entry=not args.quick)[0]
     cpu = head.get("cpu_baseline")
     torch.cuda.empty_cache()
