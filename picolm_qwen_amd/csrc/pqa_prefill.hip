@@ -661,15 +661,19 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         PQA_PSTAMP(32 * j + kPStMerged, tid == 0);
         if (par == 0) {
             {
+                // the row's 1/l folded into both weights: one multiply and one
+                // fused multiply-add per output value (the output is not stored
+                // in any reference rounding order, only within the tolerance)
                 const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
                 const float M = fmaxf(m_run, mo);
                 const float fe = fast_exp2(m_run - M);
                 const float fo = fast_exp2(mo - M);
-                l_run = l_run * fe + lo * fo;
+                const float inv = 1.0f / sum_x32(fmaf(l_run, fe, lo * fo));
+                const float we = fe * inv, wo = fo * inv;
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * fe + mg[(16 * dt + r) * 64 + lane] * fo;
+                    for (int r = 0; r < 16; r++) o[dt][r] = fmaf(o[dt][r], we, mg[(16 * dt + r) * 64 + lane] * wo);
             }
 
             // ---- normalise and store ----
@@ -679,7 +683,6 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             // writes whole 512-byte output rows instead of 32-byte pieces of 32 rows.
             constexpr int CPR = HD / 4;  // 16-byte chunks per output row
             static_assert(32 * HD <= MR * 64, "output staging exceeds the merge area");
-            const float inv = 1.0f / sum_x32(l_run);
             const int orow = rvalid ? tok * a.nh + hq : -1;  // output row of q row `col`
             wave_sync();
 #pragma unroll
@@ -688,8 +691,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 for (int r4 = 0; r4 < 4; r4++) {
                     const int c = 8 * dt + 2 * r4 + hk;  // dims 32 dt + 8 r4 + 4 hk .. +3
                     *(floatx4*)(mg + col * HD + 4 * (c ^ (col & (CPR - 1)))) =
-                        floatx4{o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
-                                o[dt][4 * r4 + 3] * inv};
+                        floatx4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
                 }
             wave_sync();
 #pragma unroll
