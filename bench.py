@@ -443,8 +443,9 @@ def host_entry_prefill(cx, q, k, v, out, s):
     t = median_time(step, 3)
     return {"entry": "pqa_prefill_host", "us_per_layer": round(t * 1e6 / cx.n_layers, 1),
             "equals_device_entry": bool(np.array_equal(oh, want)),
-            "note": "the caller's pageable host buffers (80 MB per layer, past the 4 MiB pinned staging buffer): "
-                    "three H2D copies straight from them, the prefill, one D2H copy and a stream sync per call"}
+            "note": "the caller's pageable host buffers (80 MB in, 32 MB out per layer, past the 4 MiB one-copy "
+                    "staging): streamed through two 8 MiB pinned slots (CPU threads fill one while the DMA "
+                    "engine copies the other), the prefill, the results back the same way, a stream sync per call"}
 
 
 def prefill_workload(torch, dev, n_layers, nh, nkv, hd, s, steps, warmup, seed=4242, cpu=False, host_entry=False):

@@ -3,8 +3,11 @@
 // pqa_prefill.hip and pqa_util.hip.
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <thread>
 
 #include "pqa_internal.h"
 
@@ -24,6 +27,73 @@ int hip_check(pqa_ctx* ctx, hipError_t e, const char* what) {
     return set_err(ctx, code, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// CPU threads that split large copies between pageable and pinned host
+// memory: one memcpy per thread (the calling thread takes the first piece).
+// A single thread copies ~20 GB/s on the hosts here, below what the PCIe DMA
+// of the next stage moves.
+struct CopyPool {
+    struct Piece {
+        char* dst;
+        const char* src;
+        size_t n;
+    };
+    std::vector<std::thread> threads;
+    std::vector<Piece> pieces;
+    std::mutex mu;
+    std::condition_variable go, done;
+    unsigned gen = 0;
+    int pending = 0;
+    bool quit = false;
+
+    explicit CopyPool(int workers) : pieces((size_t)workers) {
+        for (int i = 0; i < workers; ++i) threads.emplace_back([this, i] { run(i); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> l(mu);
+            quit = true;
+        }
+        go.notify_all();
+        for (auto& t : threads) t.join();
+    }
+    void run(int i) {
+        unsigned seen = 0;
+        std::unique_lock<std::mutex> l(mu);
+        for (;;) {
+            go.wait(l, [&] { return quit || gen != seen; });
+            if (quit) return;
+            seen = gen;
+            const Piece p = pieces[(size_t)i];
+            l.unlock();
+            if (p.n) std::memcpy(p.dst, p.src, p.n);
+            l.lock();
+            if (--pending == 0) done.notify_one();
+        }
+    }
+    // dst[0, n) = src[0, n)
+    void copy(char* dst, const char* src, size_t n) {
+        if (threads.empty() || n < (size_t(1) << 20)) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        const size_t parts = threads.size() + 1;
+        const size_t per = (n / parts + 63) & ~size_t(63);
+        {
+            std::lock_guard<std::mutex> l(mu);
+            for (size_t i = 0; i < threads.size(); ++i) {
+                const size_t off = std::min(n, per * (i + 1));
+                pieces[i] = Piece{dst + off, src + off, std::min(per, n - off)};
+            }
+            pending = (int)threads.size();
+            ++gen;
+        }
+        go.notify_all();
+        std::memcpy(dst, src, std::min(per, n));
+        std::unique_lock<std::mutex> l(mu);
+        done.wait(l, [&] { return pending == 0; });
+    }
+};
+
 }  // namespace pqa
 
 using pqa::hip_check;
@@ -42,7 +112,10 @@ static void free_ctx(pqa_ctx* c) {
     for (int i = 0; i < 2; ++i) {
         if (c->kvc_buf[i]) (void)hipHostFree(c->kvc_buf[i]);
         if (c->kvc_ev[i]) (void)hipEventDestroy(c->kvc_ev[i]);
+        if (c->hpipe_buf[i]) (void)hipHostFree(c->hpipe_buf[i]);
+        if (c->hpipe_ev[i]) (void)hipEventDestroy(c->hpipe_ev[i]);
     }
+    delete c->copy_pool;
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -228,8 +301,7 @@ static int ensure_stage(pqa_ctx* ctx, size_t floats) {
 // host buffer: a CPU copy into it, one host-to-device copy, the kernels, one
 // device-to-host copy. A decode call moves 2 (q_dim + kv_dim) floats, 80 KB at
 // 32 query heads of 128; every pageable copy would cost a staged transfer of
-// its own. Larger payloads (prompts) copy straight from the caller's memory,
-// where the runtime pipelines its own staging.
+// its own. Larger payloads (prompts) stream through two pinned slots (below).
 constexpr size_t kHostStageBytes = size_t(4) << 20;
 
 // The pinned staging buffer of the host entries: hipHostMallocDefault, i.e.
@@ -248,6 +320,100 @@ static int ensure_hstage(pqa_ctx* ctx, size_t floats) {
                            "pinned staging"))
         return rc;
     ctx->hstage_floats = floats;
+    return PQA_OK;
+}
+
+// Larger payloads move through two pinned slots of kPipeBytes: the CPU
+// threads fill one slot from the caller's memory while the DMA engine copies
+// the other to HBM (and the reverse for the results), so the PCIe copies run
+// at DMA speed instead of at the runtime's single-threaded staging of
+// pageable memory.
+constexpr size_t kPipeBytes = size_t(8) << 20;
+
+static int ensure_pipe(pqa_ctx* ctx, const char* fn) {
+    for (int i = 0; i < 2; ++i) {
+        if (!ctx->hpipe_buf[i]) {
+            if (int rc = hip_check(ctx, hipHostMalloc(&ctx->hpipe_buf[i], kPipeBytes, hipHostMallocDefault), fn)) {
+                ctx->hpipe_buf[i] = nullptr;
+                return rc;
+            }
+        }
+        if (!ctx->hpipe_ev[i]) {
+            if (int rc = hip_check(ctx, hipEventCreateWithFlags(&ctx->hpipe_ev[i], hipEventDisableTiming), fn)) {
+                ctx->hpipe_ev[i] = nullptr;
+                return rc;
+            }
+        }
+    }
+    if (!ctx->copy_pool) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        const int workers = (int)std::min(7u, std::max(1u, hw / 2) - 1u);
+        try {
+            ctx->copy_pool = new pqa::CopyPool(workers);
+        } catch (...) {
+            return set_err(ctx, PQA_ERR_NOMEM, std::string(fn) + ": cannot start the copy threads");
+        }
+    }
+    return PQA_OK;
+}
+
+struct HostSpan {
+    const char* p;
+    size_t n;
+};
+
+// dev[0, total) = the concatenation of spans, queued on the context stream;
+// returns once every slot is refilled for the last time (the last copies may
+// still be in flight; the caller's later stream work orders after them).
+static int pipe_to_device(pqa_ctx* ctx, char* dev, const HostSpan* spans, int nspans, const char* fn) {
+    size_t total = 0;
+    for (int i = 0; i < nspans; ++i) total += spans[i].n;
+    int si = 0;
+    size_t soff = 0;
+    for (size_t off = 0, c = 0; off < total; off += kPipeBytes, ++c) {
+        const int b = (int)(c & 1);
+        if (c >= 2)
+            if (int rc = hip_check(ctx, hipEventSynchronize(ctx->hpipe_ev[b]), fn)) return rc;
+        const size_t len = std::min(kPipeBytes, total - off);
+        char* slot = (char*)ctx->hpipe_buf[b];
+        for (size_t done = 0; done < len;) {  // gather [off, off + len) from the spans
+            const size_t m = std::min(len - done, spans[si].n - soff);
+            ctx->copy_pool->copy(slot + done, spans[si].p + soff, m);
+            done += m;
+            soff += m;
+            if (soff == spans[si].n) {
+                ++si;
+                soff = 0;
+            }
+        }
+        if (int rc = hip_check(ctx, hipMemcpyAsync(dev + off, slot, len, hipMemcpyHostToDevice, ctx->stream), fn))
+            return rc;
+        if (int rc = hip_check(ctx, hipEventRecord(ctx->hpipe_ev[b], ctx->stream), fn)) return rc;
+    }
+    return PQA_OK;
+}
+
+// host[0, total) = dev[0, total) after the work queued so far; returns when
+// every byte is in host memory.
+static int pipe_to_host(pqa_ctx* ctx, char* host, const char* dev, size_t total, const char* fn) {
+    const size_t nc = (total + kPipeBytes - 1) / kPipeBytes;
+    auto queue = [&](size_t c) {
+        const int b = (int)(c & 1);
+        const size_t off = c * kPipeBytes, len = std::min(kPipeBytes, total - off);
+        int rc = hip_check(ctx, hipMemcpyAsync(ctx->hpipe_buf[b], dev + off, len, hipMemcpyDeviceToHost, ctx->stream), fn);
+        if (!rc) rc = hip_check(ctx, hipEventRecord(ctx->hpipe_ev[b], ctx->stream), fn);
+        return rc;
+    };
+    for (size_t c = 0; c < std::min<size_t>(2, nc); ++c)
+        if (int rc = queue(c)) return rc;
+    for (size_t c = 0; c < nc; ++c) {
+        const int b = (int)(c & 1);
+        if (int rc = hip_check(ctx, hipEventSynchronize(ctx->hpipe_ev[b]), fn)) return rc;
+        const size_t off = c * kPipeBytes, len = std::min(kPipeBytes, total - off);
+        ctx->copy_pool->copy(host + off, (const char*)ctx->hpipe_buf[b], len);
+        if (c + 2 < nc)
+            if (int rc = queue(c + 2)) return rc;
+    }
     return PQA_OK;
 }
 
@@ -293,18 +459,25 @@ static int run_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool prefill, c
         std::memcpy(h + nq + nkv, v, nkv * sizeof(float));
         rc = hip_check(ctx, hipMemcpyAsync(dq, h, in_floats * sizeof(float), hipMemcpyHostToDevice, st), fn);
     } else {
-        rc = hip_check(ctx, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, st), fn);
-        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, st), fn);
-        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dv, v, nkv * 4, hipMemcpyHostToDevice, st), fn);
+        // q, k and v are contiguous in the device staging
+        const HostSpan spans[3] = {{(const char*)q, nq * 4}, {(const char*)k, nkv * 4}, {(const char*)v, nkv * 4}};
+        rc = ensure_pipe(ctx, fn);
+        if (!rc) rc = pipe_to_device(ctx, (char*)dq, spans, 3, fn);
+        if (!rc)
+            rc = prefill ? pqa_prefill(ctx, layer, pos, n_tok, dq, dk, dv, dout)
+                         : pqa_decode(ctx, layer, pos, dq, dk, dv, dout);
+        if (!rc) rc = pipe_to_host(ctx, (char*)out, (const char*)dout, nq * 4, fn);
+        (void)hipStreamSynchronize(st);  // also after a failure: no copy still uses the slots
+        return rc;
     }
     if (!rc)
         rc = prefill ? pqa_prefill(ctx, layer, pos, n_tok, dq, dk, dv, dout)
                      : pqa_decode(ctx, layer, pos, dq, dk, dv, dout);
-    float* back = pinned ? ctx->hstage + in_floats : out;
+    float* back = ctx->hstage + in_floats;
     if (!rc) rc = hip_check(ctx, hipMemcpyAsync(back, dout, nq * 4, hipMemcpyDeviceToHost, st), fn);
     if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
-    else if (pinned) (void)hipStreamSynchronize(st);  // a failed call leaves no copy reading the buffer
-    if (!rc && pinned) std::memcpy(out, back, nq * sizeof(float));
+    else (void)hipStreamSynchronize(st);  // a failed call leaves no copy reading the buffer
+    if (!rc) std::memcpy(out, back, nq * sizeof(float));
     return rc;
 }
 
@@ -336,16 +509,25 @@ static int run_block_host(pqa_ctx* ctx, int layer, int pos, int n_tok, bool pref
         std::memcpy(h + n4, x, n * sizeof(float));
         rc = hip_check(ctx, hipMemcpyAsync(dxb, h, (n4 + n) * sizeof(float), hipMemcpyHostToDevice, st), fn);
     } else {
-        rc = hip_check(ctx, hipMemcpyAsync(dxb, xb, n * sizeof(float), hipMemcpyHostToDevice, st), fn);
-        if (!rc) rc = hip_check(ctx, hipMemcpyAsync(dx, x, n * sizeof(float), hipMemcpyHostToDevice, st), fn);
+        // xb, then x at its 16-byte aligned offset n4
+        static const float zero_pad[3] = {0.0f, 0.0f, 0.0f};
+        const HostSpan spans[3] = {{(const char*)xb, n * 4}, {(const char*)zero_pad, (n4 - n) * 4}, {(const char*)x, n * 4}};
+        rc = ensure_pipe(ctx, fn);
+        if (!rc) rc = pipe_to_device(ctx, (char*)dxb, spans, 3, fn);
+        if (!rc)
+            rc = prefill ? pqa_prefill_block(ctx, layer, pos, n_tok, dxb, dx)
+                         : pqa_attention_block(ctx, layer, pos, dxb, dx);
+        if (!rc) rc = pipe_to_host(ctx, (char*)x, (const char*)dx, n * 4, fn);
+        (void)hipStreamSynchronize(st);  // also after a failure: no copy still uses the slots
+        return rc;
     }
     if (!rc)
         rc = prefill ? pqa_prefill_block(ctx, layer, pos, n_tok, dxb, dx) : pqa_attention_block(ctx, layer, pos, dxb, dx);
-    float* back = pinned ? ctx->hstage + n4 + n : x;
+    float* back = ctx->hstage + n4 + n;
     if (!rc) rc = hip_check(ctx, hipMemcpyAsync(back, dx, n * sizeof(float), hipMemcpyDeviceToHost, st), fn);
     if (!rc) rc = hip_check(ctx, hipStreamSynchronize(st), fn);
     else (void)hipStreamSynchronize(st);  // a failed call leaves no copy reading the buffers
-    if (!rc && pinned) std::memcpy(x, back, n * sizeof(float));
+    if (!rc) std::memcpy(x, back, n * sizeof(float));
     return rc;
 }
 

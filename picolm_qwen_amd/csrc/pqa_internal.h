@@ -36,6 +36,10 @@ struct pqa_proj_weights {
     float* exact = nullptr;
 };
 
+namespace pqa {
+struct CopyPool;  // pqa_api.hip
+}
+
 struct pqa_ctx {
     int n_layers = 0, max_seq_len = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, rope_style = 0;
     int kv_mul = 1;            // query heads per KV head (cpp/model.hpp:295)
@@ -97,6 +101,13 @@ struct pqa_ctx {
     // made on the first pqa_kvc_save / pqa_kvc_load
     void* kvc_buf[2] = {nullptr, nullptr};
     hipEvent_t kvc_ev[2] = {nullptr, nullptr};
+
+    // host entries with payloads past the one-copy staging (prompts): two
+    // pinned slots, their copy events and the CPU threads that fill and drain
+    // them; made on the first such call
+    void* hpipe_buf[2] = {nullptr, nullptr};
+    hipEvent_t hpipe_ev[2] = {nullptr, nullptr};
+    pqa::CopyPool* copy_pool = nullptr;
 
     hipStream_t stream = nullptr;
     int device = 0;

@@ -118,14 +118,17 @@ def test_prefill_block_matches_oracle_chain_and_its_halves():
         a.close()
 
 
-@pytest.mark.parametrize("n_tok", [24, 300])
+@pytest.mark.parametrize("n_tok", [24, 300, 1100])
 def test_host_entry_points_equal_device_ones(n_tok):
     # pqa_prefill_block_host / pqa_attention_block_host against the device
-    # forms on a twin context: bit-equal x and cache rows. 300 tokens of 2048
-    # floats (three 2.4 MB copies) take the unpinned copy path, 24 the pinned one
+    # forms on a twin context: bit-equal x and cache rows. 24 tokens take the
+    # one-copy pinned buffer; 300 tokens of 2048 floats (4.8 MB in, 2.4 MB
+    # back) one fill of the two 8 MiB slots each way; 1100 tokens (18 MB in,
+    # 9 MB back) three fills in and two back
     print(f"host blocks n_tok {n_tok}", flush=True)
     rng = np.random.default_rng(777 + n_tok)
-    nh, nkv, hd, dim, smax = 16, 4, 128, 2048, 320
+    nh, nkv, hd, dim = 16, 4, 128, 2048
+    smax = max(320, n_tok + 8)
     types = (O.GGUF_Q8_0, O.GGUF_Q8_0, O.GGUF_Q8_0, O.GGUF_Q4_K)
     w, b = _layer(rng, nh, nkv, hd, dim, types, bias=True)
     cos, sin = O.rope_table(1e6, hd, smax)

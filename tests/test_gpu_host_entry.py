@@ -1,8 +1,9 @@
 """The host-pointer entry points (pqa_decode_host, pqa_prefill_host), the calls
 a CPU forward loop makes per layer in place of cpp/model.hpp:326-418 and
 :489-593. Small payloads travel through one pinned host buffer, large ones
-straight from the caller's memory; both must give the device-pointer entry's
-bits exactly, and the K/V rows they append must be the same."""
+through two pinned 8 MiB slots that CPU threads fill while the DMA engine
+drains the other; both must give the device-pointer entry's bits exactly, and
+the K/V rows they append must be the same."""
 import numpy as np
 import pytest
 import torch
@@ -28,9 +29,12 @@ def _device(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
 
 
-@pytest.mark.parametrize("n_tok", [3, 300])  # 300 x 20 KB of payload: past the 4 MiB pinned buffer
+# 300 x 20 KB of payload: past the 4 MiB one-copy buffer, one slot each way;
+# 2400 tokens: 28.8 MB in (four slot fills, both slots reused) and 19.2 MB out
+@pytest.mark.parametrize("n_tok", [3, 300, 2400])
 def test_prefill_host_matches_device_entry(n_tok):
-    nh, nkv, hd, smax, seed = 16, 4, 128, 512, 7301
+    nh, nkv, hd, seed = 16, 4, 128, 7301
+    smax = max(512, n_tok)
     host, dev = _pair(nh, nkv, hd, smax, seed)
     q, k, v = O.batch_inputs(seed, 0, 0, n_tok, nh, nkv, hd)
     got = host.forward_batch(0, 0, q, k, v)
