@@ -232,9 +232,12 @@ int pqa_attention_block(pqa_ctx* ctx, int layer, int pos, const float* xb, float
  * library's gemm_f16x3_nt_kernel, fp16 MFMA, fp32 accumulation) sums
  * w_hi x_hi + w_hi x_lo + w_lo x_hi; the
  * scale is undone exactly and the bias added. The error stays within
- * (3 n_embd + 12) 2^-24 sum |w x|, so q/k/v agree with the reference to fp32
+ * (3 n_embd + 12) 2^-24 sum |w x|, so q agrees with the reference to fp32
  * rounding (about 1e-6 relative), not bit for bit (pqa_qkv_project keeps the
- * order for one token). DEVICE pointers xb [n_tok][n_embd], q [n_tok][q_dim],
+ * order for one token). k and v follow pqa_set_batch_projection: by default
+ * in the reference's own order, bit-identical to pqa_qkv_project's, so the
+ * cache rows a prompt writes are the reference's; with exact_kv = 0 on the
+ * same GEMM as q. DEVICE pointers xb [n_tok][n_embd], q [n_tok][q_dim],
  * k and v [n_tok][kv_dim]; asynchronous on the context stream.
  * Memory: the first call for a layer keeps that layer's split weights,
  * about (q_dim + 2 kv_dim) * (4 n_embd + 4) bytes, until its weights are
