@@ -28,6 +28,10 @@ CASES = [
     ("g1_interleaved_n65", 4, 4, 64, 96, 2, 1e4, False, 0, 65, 0.0),
     ("block8_hd128_splitq_n150", 16, 4, 128, 200, 1, 1e4, True, 3, 150, 0.01),
     ("interleaved_hd64_splitq_n130", 8, 2, 64, 160, 2, 1e4, True, 0, 130, 0.01),
+    # Llama-3.2-1B heads: 8 KV heads at hd 64, 1200 rows in 10 row blocks
+    ("llama32_1b_hd64_start20_n300", 32, 8, 64, 512, 0, 5e5, False, 20, 300, 0.0),
+    # 4000 rows in 32 row blocks behind a 50-row history
+    ("qwen3_4b_start50_n1000", 32, 8, 128, 1100, 0, 1e6, True, 50, 1000, 0.0),
 ]
 
 
@@ -136,3 +140,34 @@ def test_prefill_row_equals_decode():
     assert_bits_equal(va, vb, "V rows prefill vs decode")
     a.close()
     b.close()
+
+
+def test_prefill_successive_launches_append_every_row():
+    # two layers, the prompt in two chunks per layer with the layers
+    # interleaved (Qwen3-4B heads): every launch appends all of its rows,
+    # bit-equal to the oracle's, and its outputs, which read the previous
+    # chunk's rows as history, are within the tolerance
+    print("prefill successive launches", flush=True)
+    nh, nkv, hd, smax, seed = 32, 8, 128, 640, 9100
+    kvd = nkv * hd
+    cos, sin = O.rope_table(1e6, hd, smax)
+    att = PicoAttention(2, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin)
+    norms = [O.qk_norm_weights(seed, layer, hd) for layer in range(2)]
+    for layer in range(2):
+        att.set_qk_norm(layer, *norms[layer])
+    kc = np.zeros((2, smax, kvd), np.uint16)
+    vc = np.zeros_like(kc)
+    shp = O.shape(nh, nkv, hd, smax, 0)
+    dev = torch.device("cuda:0")
+    for start, n in ((0, 256), (256, 344)):
+        for layer in range(2):
+            q, k, v = O.batch_inputs(seed, layer, start, n, nh, nkv, hd)
+            out = att.forward_batch(layer, start, *(torch.from_numpy(x).to(dev) for x in (q, k, v)))
+            torch.cuda.synchronize()
+            want = O.prefill(shp, start, q, k, v, *norms[layer], cos, sin, kc[layer], vc[layer],
+                             n_threads=cpu_threads())
+            gk, gv = att.kv_download(layer, start, n)
+            assert_bits_equal(gk, kc[layer, start:start + n], f"K rows layer {layer} from {start}")
+            assert_bits_equal(gv, vc[layer, start:start + n], f"V rows layer {layer} from {start}")
+            assert_close(out.cpu().numpy(), want, what=f"layer {layer} from {start}")
+    att.close()
