@@ -37,7 +37,7 @@ struct pqa_proj_weights {
 };
 
 namespace pqa {
-struct CopyPool;  // pqa_api.hip
+struct CopyPool;  // pqa_copy_pool.h
 }
 
 struct pqa_ctx {
