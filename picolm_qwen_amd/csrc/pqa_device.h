@@ -196,6 +196,17 @@ __device__ __forceinline__ void lds_dma_b128(const void* base, unsigned voff, un
                  : "memory", "m0");
 }
 
+// The same with the non-temporal hint: data read once (streaming), kept from
+// displacing reused lines in the caches.
+__device__ __forceinline__ void lds_dma_b128_nt(const void* base, unsigned voff, unsigned lds) {
+    base = uniform_ptr(base);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
 // 4 bytes per lane (global_load_lds_dword): lane l's dword lands at LDS byte
 // address lds + 4 l. Same contract as lds_dma_b128.
 __device__ __forceinline__ void lds_dma_b32(const void* base, unsigned voff, unsigned lds) {

@@ -204,6 +204,17 @@ struct AttnArgs {
     int qbt;
 };
 
+// The prompt's q rows and output rows each cross the chip once: read and
+// stored with the non-temporal hint, they stay out of the way of the K/V
+// tiles that 32 workgroups share, and the output leaves no dirty lines behind
+// for the next launch. Qwen3-4B prefill, per layer: 70.6 -> 68.9 us (attention
+// 64.6-64.8 -> 62.9-63.3 us, the next layer's K/V prep 7.45 -> 7.24 us); the
+// q hint alone changed nothing measurable.
+#ifndef PQA_PF_NT
+#define PQA_PF_NT 3
+#endif
+constexpr bool kNtQ = (PQA_PF_NT & 1) != 0;    // q rows read with the non-temporal hint
+constexpr bool kNtOut = (PQA_PF_NT & 2) != 0;  // output rows stored with it
 constexpr int kAttnThreads = 512;  // 2 groups of 4 waves: even and odd key tiles
 constexpr int kGroupWaves = 4;
 constexpr int kRowsPerBlock = 128;
@@ -372,7 +383,8 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             const int tq = Rq / a.g;
             const unsigned qoff = (unsigned)(((tq - tq0) * a.q_ld + (kvh * a.g + (Rq - tq * a.g)) * HD) * 4);
             const int c = (lane % CQ) ^ (rr & (CQ - 1));
-            lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
+            if constexpr (kNtQ) lds_dma_b128_nt(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
+            else lds_dma_b128(qbase, qoff + 16u * c, lds_addr(qst + j * 1024));
         }
         constexpr int NF = HD / 16;       // float4s per lane: NF/2 in each half
         constexpr int NH4 = NF / 2;       // float4s per half
@@ -705,7 +717,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                     if (lane / CPR == u) orr = v;
                 }
                 const floatx4 vv = *(const floatx4*)(mg + rr * HD + 4 * (c ^ (rr & (CPR - 1))));
-                if (orr >= 0) *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv;
+                if (orr >= 0) {
+                    if constexpr (kNtOut) __builtin_nontemporal_store(vv, (floatx4*)(a.out + (size_t)orr * HD + 4 * c));
+                    else *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv;
+                }
             }
             PQA_PSTAMP(32 * j + kPStStored + w, lane == 0);
         }
