@@ -1106,7 +1106,54 @@ def prefill_phase_stamps(reps=5):
         lines.append(f"    partials merged {med[b + 17]:6.2f}")
         lines.append("    rows stored     " + " ".join(f"{x:6.2f}" for x in med[b + 18:b + 22]))
     cx.close()
+    lines += prefill_step_stamps(reps)
     return "\n".join(lines)
+
+
+SSTAMP_WGS, SSTAMP_STEPS, SSTAMP_EVENTS = 256, 32, 8
+
+
+def prefill_step_stamps(reps):
+    """Per-step phases of the long block's tile loop, from the build with the
+    per-step stamps (waves 0 and 4 of the first 256 workgroups), on the same
+    prefill: the mean time of each phase of a step, in ns, over every stamped
+    step of every workgroup, median of reps launches. The stamps cost time
+    themselves, so this build runs slower than the one without them."""
+    import torch
+    from picolm_qwen_amd import _lib
+    L = _lib.stamped_lib(step=True)
+    dev = torch.device("cuda:0")
+    nh, nkv, hd, s = 32, 8, 128, 2048
+    cx = Ctx(1, s, nh, nkv, hd, 0, 1e6, L=L)
+    rng = np.random.default_rng(4242)
+    set_norms(cx, rng, hd)
+    q, k, v, out = make_inputs(torch, dev, rng, 1, s, nh, nkv, hd)
+    torch.cuda.synchronize()
+    args = [C.c_void_p(t[0].data_ptr()) for t in (q, k, v, out)]
+    _, ev = timed(torch, cx, lambda: L.pqa_prefill(cx.h, 0, 0, s, *args), 10, 3)
+    names = ["wait for own tile loads", "workgroup barrier", "issue next tile loads", "score MFMAs + row max",
+             "exp, fp16 P, row sums", "PV MFMAs issued", "to the next step"]
+    per = []
+    for _ in range(reps):
+        cx.check(L.pqa_prefill_stamps_clear())
+        cx.check(L.pqa_prefill(cx.h, 0, 0, s, *args), cx.h)
+        cx.check(L.pqa_sync(cx.h), cx.h)
+        a = np.zeros(SSTAMP_WGS * 2 * SSTAMP_STEPS * SSTAMP_EVENTS, np.uint64)
+        cx.check(L.pqa_prefill_step_stamps_read(a.ctypes.data_as(C.c_void_p), a.size))
+        a = a.reshape(SSTAMP_WGS * 2, SSTAMP_STEPS, SSTAMP_EVENTS).astype(np.float64)
+        a[a == 0] = np.nan
+        nxt = np.concatenate([a[:, 1:, 0], np.full((a.shape[0], 1), np.nan)], 1)  # next step's start
+        d = np.diff(np.concatenate([a[:, :, :7], nxt[:, :, None]], 2), axis=2) * 10.0  # 100 MHz ticks -> ns
+        per.append(np.nanmean(d.reshape(-1, 7), 0))
+    m = np.median(np.stack(per), 0)
+    cx.close()
+    lines = [f"  long-block tile loop, per step (both waves of a SIMD one 64-key tile each; the build with per-step "
+             f"stamps: {ev * 1e3:.1f} us per call event-timed): mean ns per phase over waves 0 and 4 of every "
+             f"workgroup, median of {reps} launches"]
+    for nm, x in zip(names, m):
+        lines.append(f"    {nm:28s} {x:7.1f}")
+    lines.append(f"    {'step total':28s} {float(np.nansum(m)):7.1f}")
+    return lines
 
 
 def phase_stamps(cases=None, reps=7):

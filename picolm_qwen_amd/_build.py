@@ -14,6 +14,10 @@ LIB = os.path.join(PKG, "libpqa.so")
 # the same sources with -DPQA_PHASE_STAMPS: kernels also write s_memrealtime
 # stamps at their phase boundaries (measurement only, bench.py --phase-stamps)
 STAMPS_LIB = os.path.join(PKG, "libpqa_stamps.so")
+# the stamped build with the prefill tile loop's per-step stamps as well
+# (-DPQA_STEP_STAMPS; they cost time, so the per-phase stamps come from the
+# build without them)
+STEP_STAMPS_LIB = os.path.join(PKG, "libpqa_stepstamps.so")
 SOURCES = ["pqa_api.hip", "pqa_decode.hip", "pqa_prefill.hip", "pqa_util.hip", "pqa_kvc.hip", "pqa_proj.hip", "pqa_batch.hip",
            "pqa_gemm.hip", "pqa_general.hip", "pqa_exact.hip"]
 
@@ -37,11 +41,12 @@ def _compile(src: str, obj: str, extra=()) -> None:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
 
 
-def build(verbose: bool = False, stamps: bool = False) -> str:
+def build(verbose: bool = False, stamps: bool = False, step_stamps: bool = False) -> str:
     """Compiles every csrc/*.hip source and links libpqa.so (with stamps:
-    libpqa_stamps.so, the phase-stamped variant); returns its path."""
-    out = STAMPS_LIB if stamps else LIB
-    extra = ["-DPQA_PHASE_STAMPS"] if stamps else []
+    libpqa_stamps.so, the phase-stamped variant; with step_stamps as well:
+    libpqa_stepstamps.so); returns its path."""
+    out = (STEP_STAMPS_LIB if step_stamps else STAMPS_LIB) if stamps else LIB
+    extra = (["-DPQA_PHASE_STAMPS"] + (["-DPQA_STEP_STAMPS"] if step_stamps else [])) if stamps else []
     with tempfile.TemporaryDirectory(prefix="pqa_build_") as tmp:
         objs = [os.path.join(tmp, s.replace(".hip", ".o")) for s in SOURCES]
         with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
@@ -90,6 +95,7 @@ if __name__ == "__main__":
 
     if "--stamps" in sys.argv:
         build(verbose=True, stamps=True)
+        build(verbose=True, stamps=True, step_stamps=True)
         sys.exit(0)
     build(verbose=True)
     build_adapter()

@@ -5,7 +5,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-from ._build import LIB, STAMPS_LIB
+from ._build import LIB, STAMPS_LIB, STEP_STAMPS_LIB
 
 PQA_OK = 0
 PQA_ERR_ARG = -1
@@ -37,6 +37,7 @@ class PQAError(RuntimeError):
 
 _lib = None
 _stamped = None
+_step_stamped = None
 
 
 def lib() -> C.CDLL:
@@ -48,15 +49,18 @@ def lib() -> C.CDLL:
     return _lib
 
 
-def stamped_lib() -> C.CDLL:
+def stamped_lib(step: bool = False) -> C.CDLL:
     """The phase-stamped build of the same sources (measurement only: its
     kernels also write s_memrealtime stamps; pqa_decode_stamps_read /
-    pqa_prefill_stamps_read return them, the _clear calls zero them)."""
-    global _stamped
-    if _stamped is None:
-        if not os.path.exists(STAMPS_LIB):
-            raise RuntimeError(f"{STAMPS_LIB} is not built; run python -m picolm_qwen_amd._build --stamps")
-        L = _bind(C.CDLL(STAMPS_LIB))
+    pqa_prefill_stamps_read return them, the _clear calls zero them). With
+    step: the build that also stamps each step of the prefill tile loop
+    (pqa_prefill_step_stamps_read)."""
+    global _stamped, _step_stamped
+    if (_step_stamped if step else _stamped) is None:
+        path = STEP_STAMPS_LIB if step else STAMPS_LIB
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built; run python -m picolm_qwen_amd._build --stamps")
+        L = _bind(C.CDLL(path))
         L.pqa_decode_stamps_read.argtypes = [C.c_void_p, C.c_int]
         L.pqa_decode_stamps_read.restype = C.c_int
         L.pqa_decode_stamps_clear.argtypes = []
@@ -65,8 +69,13 @@ def stamped_lib() -> C.CDLL:
         L.pqa_prefill_stamps_read.restype = C.c_int
         L.pqa_prefill_stamps_clear.argtypes = []
         L.pqa_prefill_stamps_clear.restype = C.c_int
-        _stamped = L
-    return _stamped
+        L.pqa_prefill_step_stamps_read.argtypes = [C.c_void_p, C.c_int]
+        L.pqa_prefill_step_stamps_read.restype = C.c_int
+        if step:
+            _step_stamped = L
+        else:
+            _stamped = L
+    return _step_stamped if step else _stamped
 
 
 def _bind(L: C.CDLL) -> C.CDLL:

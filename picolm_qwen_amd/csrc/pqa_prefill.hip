@@ -172,14 +172,45 @@ enum : int {
     kPStQLanded = 22,  // wave 0: raw q rows (and the first tiles) landed in LDS
     kPStQMath = 23,    // wave 0: q normed, rotated and written as fp16
 };
+// Per-step stamps of the long block's tile loop, compiled in only with
+// -DPQA_STEP_STAMPS as well (bench.py --phase-stamps reads them from the
+// library built that way), so that the per-block stamps are taken without
+// their cost: waves 0 (even tiles) and 4 (odd tiles) of the first
+// kSStampWGs workgroups stamp kSStampEvents points of each of the first
+// kSStampSteps steps.
+constexpr int kSStampWGs = 256, kSStampSteps = 32, kSStampEvents = 8;
+enum : int {
+    kSStStart = 0,    // tile() entered
+    kSStLanded = 1,   // after the wave's s_waitcnt for its tile loads
+    kSStBarrier = 2,  // after the workgroup barrier
+    kSStIssued = 3,   // the next tile's loads issued
+    kSStScores = 4,   // score MFMAs done and the row maximum taken
+    kSStSoftmax = 5,  // P in fp16 and the row sums done
+    kSStPV = 6,       // PV MFMAs issued
+};
 #ifdef PQA_PHASE_STAMPS
 static __device__ unsigned long long g_prefill_stamps[kPStampWGs * kPStampSlots];
+static __device__ unsigned long long g_prefill_step_stamps[kSStampWGs * 2 * kSStampSteps * kSStampEvents];
 #define PQA_PSTAMP(slot, cond)                                                                           \
     do {                                                                                                 \
         if ((cond) && blockIdx.x < (unsigned)kPStampWGs)                                                 \
             g_prefill_stamps[(size_t)blockIdx.x * kPStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
+#endif
+#if defined(PQA_PHASE_STAMPS) && defined(PQA_STEP_STAMPS)
+#define PQA_SSTAMP(stepv, ev)                                                                                  \
+    do {                                                                                                       \
+        if (j == 0 && (tid & 63) == 0 && (w & 3) == 0 && (stepv) < kSStampSteps &&                             \
+            blockIdx.x < (unsigned)kSStampWGs)                                                                 \
+            g_prefill_step_stamps[(((size_t)blockIdx.x * 2 + (w >> 2)) * kSStampSteps + (stepv)) * kSStampEvents + \
+                                  (ev)] = __builtin_amdgcn_s_memrealtime();                                    \
+    } while (0)
 #else
+#define PQA_SSTAMP(stepv, ev) \
+    do {                      \
+    } while (0)
+#endif
+#ifndef PQA_PHASE_STAMPS
 #define PQA_PSTAMP(slot, cond) \
     do {                       \
     } while (0)
@@ -537,9 +568,13 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             constexpr int buf = decltype(BUF)::value;
             const int kt = 2 * step + par;
             const int key0 = kt * kKeysPerTile;
+            PQA_SSTAMP(step, kSStStart);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of step `step`
+            PQA_SSTAMP(step, kSStLanded);
             __syncthreads();                                   // everyone's; the other buffer is free
+            PQA_SSTAMP(step, kSStBarrier);
             issue(step + 1, buf ^ 1);
+            PQA_SSTAMP(step, kSStIssued);
             if (kt >= ntiles || key0 >= kend_w) return;  // wave-uniform: nothing left for this wave
 
             const char* kt_lds = lds[buf][par][0];
@@ -597,6 +632,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
 #pragma unroll
                 for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
             mx = max_x32(mx);
+            PQA_SSTAMP(step, kSStScores);
             if (__any(mx > m_run + kRescaleSlack)) {
                 const float m_new = fmaxf(m_run, mx);
                 const float corr = fast_exp2(m_run - m_new);
@@ -621,6 +657,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 for (int e = 0; e < 4; e++)
                     ps[s] = __builtin_amdgcn_fdot2(half2{pf[s][2 * e], pf[s][2 * e + 1]}, one2, ps[s], false);
             l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+            PQA_SSTAMP(step, kSStSoftmax);
             // O^T += V^T P^T: 4 key steps x DT dim tiles; V^T fragments (two
             // transposing reads each) through a ring RV MFMAs deep.
             constexpr int NPV = 4 * DT, RV = 4;
@@ -646,6 +683,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 __builtin_amdgcn_sched_barrier(0);
                 o[idx % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[idx / DT], o[idx % DT], 0, 0, 0);
             }
+            PQA_SSTAMP(step, kSStPV);
         };
 
         const int nsteps = (ntiles + 1) / 2;
@@ -736,10 +774,20 @@ extern "C" int pqa_prefill_stamps_read(unsigned long long* dst, int n) {
                ? PQA_OK
                : PQA_ERR_HIP;
 }
+extern "C" int pqa_prefill_step_stamps_read(unsigned long long* dst, int n) {
+    if (!dst || n != kSStampWGs * 2 * kSStampSteps * kSStampEvents) return PQA_ERR_ARG;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_prefill_step_stamps), (size_t)n * 8, 0, hipMemcpyDeviceToHost) ==
+                   hipSuccess
+               ? PQA_OK
+               : PQA_ERR_HIP;
+}
 extern "C" int pqa_prefill_stamps_clear() {
     static unsigned long long zero[kPStampWGs * kPStampSlots];
+    static_assert(sizeof(zero) >= sizeof(g_prefill_step_stamps), "one zero buffer clears both");
     return hipMemcpyToSymbol(HIP_SYMBOL(g_prefill_stamps), zero, sizeof(zero), 0, hipMemcpyHostToDevice) ==
-                   hipSuccess
+                           hipSuccess &&
+                   hipMemcpyToSymbol(HIP_SYMBOL(g_prefill_step_stamps), zero, sizeof(g_prefill_step_stamps), 0,
+                                     hipMemcpyHostToDevice) == hipSuccess
                ? PQA_OK
                : PQA_ERR_HIP;
 }
