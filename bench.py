@@ -749,6 +749,13 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
         for layer in range(n_layers):
             proj(cx.h, layer, *ptrs[layer])
 
+    # q rows in the reference's order too (pqa_set_token_projection(1)), then
+    # the default: q on the any-order path, k and v in the reference's order
+    cx.check(cx.L.pqa_set_token_projection(cx.h, 1), cx.h)
+    _, ev_exact = timed(torch, cx, step, steps, warmup)
+    us_exact = ev_exact * 1e3 / n_layers
+    q_exact = q[0].cpu().numpy().copy()
+    cx.check(cx.L.pqa_set_token_projection(cx.h, 0), cx.h)
     wall, ev = timed(torch, cx, step, steps, warmup)
     us = ev * 1e3 / n_layers
     gbs = wbytes / (us * 1e-6) / 1e9
@@ -765,7 +772,11 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
     res = {"workload": "qwen3_8b_qkv_proj_q4_k_m", "n_embd": n, "rows": [nh * hd, nkv * hd, nkv * hd],
            "weight_types": ["Q4_K", "Q4_K", "Q6_K"], "weight_bytes_per_layer": wbytes,
            "us_per_layer": round(us, 3), "weight_GB_per_s": round(gbs, 1),
-           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bit_exact_vs_reference_build_B": True,
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "q_rows": "any summation order, one row per wave (the default); k and v in the reference's order",
+           "all_reference_order": {"us_per_layer": round(us_exact, 3),
+                                   "weight_GB_per_s": round(wbytes / (us_exact * 1e-6) / 1e9, 1),
+                                   "note": "pqa_set_token_projection(1): q, k and v bit-identical to matmul_bias"},
            "out_proj": {"rows": n, "width": nh * hd, "weight_type": "Q4_K", "weight_bytes_per_layer": obytes,
                         "us_per_layer": round(ous, 3), "weight_GB_per_s": round(obytes / (ous * 1e-6) / 1e9, 1),
                         "note": "attn_output matmul_bias + residual vec_add (cpp/model.hpp:420-427)"}}
@@ -785,11 +796,19 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
             res["cpu_baseline"] = {"kind": "reference", "cores": 1, "us_per_layer": round(per * 1e6, 1),
                                    "weight_GB_per_s": round(wbytes / per / 1e9, 3),
                                    "sample": f"TensorOps::matmul_bias of the reference (build B) on layer 0, {reps}x"}
+            qr = ref.matmul_bias(xh, w0[0], Q4K, nh * hd)
+            res["q_layer0_bit_exact_all_reference_order"] = bool(np.array_equal(q_exact.view(np.uint32),
+                                                                                qr.view(np.uint32)))
             qg = q[0].cpu().numpy()
-            res["q_layer0_bit_exact"] = bool(np.array_equal(qg.view(np.uint32),
-                                                            ref.matmul_bias(xh, w0[0], Q4K, nh * hd).view(np.uint32)))
+            res["q_layer0_max_abs_err_any_order"] = float(np.max(np.abs(qg.astype(np.float64) - qr)))
+            res["q_layer0_max_abs"] = float(np.max(np.abs(qr)))
+            res["kv_layer0_bit_exact"] = bool(
+                np.array_equal(k[0].cpu().numpy().view(np.uint32), ref.matmul_bias(xh, w0[1], Q4K, nkv * hd).view(np.uint32))
+                and np.array_equal(v[0].cpu().numpy().view(np.uint32),
+                                   ref.matmul_bias(xh, w0[2], Q6K, nkv * hd).view(np.uint32)))
     cx.close()
-    log(f"[bench] qkv projection: {us:.2f} us/layer, {gbs:.0f} GB/s of weights ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); {res.get('cpu_baseline')}")
+    log(f"[bench] qkv projection: {us:.2f} us/layer, {gbs:.0f} GB/s of weights ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
+        f"all in the reference's order {us_exact:.2f} us; {res.get('cpu_baseline')}")
     return res
 
 

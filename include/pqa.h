@@ -194,8 +194,23 @@ int pqa_set_qkv_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wq, int
 /* q = Wq xb + bq, k = Wk xb + bk, v = Wv xb + bv for one token (the
  * matmul_bias calls of cpp/model.hpp:320-323, :337-340, :362-365). DEVICE
  * pointers xb [n_embd], q [n_heads*head_dim], k and v [n_kv_heads*head_dim];
- * asynchronous on the context stream. */
+ * asynchronous on the context stream. k and v are the reference's bits (its
+ * summation order, cpp/quant.hpp:297-356); q follows
+ * pqa_set_token_projection. */
 int pqa_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q, float* k, float* v);
+
+/*
+ * How pqa_qkv_project (and pqa_decode_x, pqa_attention_block and their host
+ * forms, which call it) computes q.
+ * 0 (default): q rows of type F32, F16 or Q4_K are summed in any order on a
+ *    bandwidth-bound path (one row per wave), within (n_embd + 12) 2^-24
+ *    sum_i |w_i x_i| of the reference's sum; q only feeds the attention
+ *    scores, so no cache row depends on its bits. Other q types, and k and v
+ *    always, keep the reference's order.
+ * 1: q in the reference's order too, bit-identical to matmul_bias.
+ * No counterpart in the reference, which has one order only.
+ */
+int pqa_set_token_projection(pqa_ctx* ctx, int exact_q);
 
 /* The attention block of Model::forward from the normed input on
  * (cpp/model.hpp:320-418): pqa_qkv_project into a context workspace, then

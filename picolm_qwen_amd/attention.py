@@ -216,6 +216,14 @@ class PicoAttention:
         land one fp16 step off)."""
         check(lib().pqa_set_batch_projection(self.handle, int(bool(exact_kv))), self.handle)
 
+    def set_token_projection(self, exact_q: bool) -> None:
+        """False (the default): the one-token projections sum the q rows of
+        F32, F16 and Q4_K in any order on a bandwidth-bound path (within the
+        fp32 reordering bound; q only feeds scores); True: q in the
+        reference's order too, bit-identical to matmul_bias. k and v keep the
+        reference's order either way."""
+        check(lib().pqa_set_token_projection(self.handle, int(bool(exact_q))), self.handle)
+
     # -- the block ----------------------------------------------------------
     def set_qk_norm(self, layer: int, q_norm_w, k_norm_w) -> None:
         """Layer's attn_q_norm / attn_k_norm weights ([head_dim] each); None turns it off."""

@@ -66,6 +66,12 @@ struct pqa_ctx {
     // whose score error grows with |q| |k|
     int prefill_split_q = 1;
 
+    // one-token projections (pqa_qkv_project and the entries built on it): 0
+    // (default) q rows of F32, F16 and Q4_K summed in any order on a
+    // bandwidth-bound path, k and v in the reference's order; 1 all three in
+    // the reference's order
+    int token_exact_q = 0;
+
     // batched projections: 1 (default) the K and V columns in the reference's
     // summation order (bit-exact cache rows), q on the split fp16 GEMM; 0 all
     // three on the split GEMM

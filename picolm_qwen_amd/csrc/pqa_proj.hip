@@ -51,6 +51,7 @@ struct ProjMat {
     float* out;        // with add_out: out[row] += result (vec_add into the residual stream)
     int add_out;
     int rows, wtype, btype, stride, wg0;  // wg0: first workgroup of this matrix
+    int fast;  // rows summed in any order (gemv_wg), one row per wave; else the reference's order (proj_wg)
 };
 
 struct ProjArgs {
@@ -327,6 +328,157 @@ __device__ void proj_wg(const ProjMat& m, const float* __restrict__ x, float* xs
     }
 }
 
+// The q rows of one token without the fixed order. q feeds only the
+// attention scores (its bits reach no cache row), so its sums may take any
+// order: one row per wave, the lanes over interleaved units of the row (a
+// float4 of F32, 8 halfs of F16, a quarter block of Q4_K: its 16-byte header
+// and 32 quant bytes, 64 elements), one fp32 fused sum per lane, then a
+// butterfly sum over the wave and the bias. Every weight byte is read once,
+// x comes from LDS. F32 and F16 weights multiply x as they are; a Q4_K
+// group of 32 elements w = d q - m (cpp/quant.hpp:220-236) contributes
+// d sum q x - m sum x, with sum x per group computed once per workgroup.
+// Error against the reference's order: at most (n + 12) 2^-24 sum_i |w_i x_i|
+// for F32 and F16, and (n + 12) 2^-24 sum_i (|d q_i| + |m|) |x_i| for Q4_K.
+__host__ __device__ constexpr bool gemv_type(int t) { return t == GG_F32 || t == GG_F16 || t == GG_Q4_K; }
+
+template <int T>
+__device__ void gemv_wg(const ProjMat& m, const float* __restrict__ x, float* xs, int n, int lwg) {
+    static_assert(gemv_type(T), "types with 16-byte aligned units");
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row = lwg * kProjWaves + w;
+    // waves past the last row load the last row again and store nothing: every
+    // wave reaches the barrier below
+    const uint8_t* wr = m.w + (size_t)min(row, m.rows - 1) * m.stride;
+    // F32 / F16: lane l takes unit l + 64 k of EU elements (n is a multiple of
+    // 8, so a unit is whole or past the row), 8 units per batch. Q4_K: unit
+    // u = 4 sb + jj is the quarter block of elements 256 sb + 64 jj + [0, 64)
+    // (cpp/quant.hpp:220-236), its 16-byte header and 32 quant bytes; n <= 8192
+    // gives at most 2 units per lane.
+    constexpr int EU = T == GG_F32 ? 4 : 8;
+    constexpr int NB = T == GG_Q4_K ? 6 : 8;  // 16-byte loads held per lane
+    u32x4 wv[NB];
+    auto load_batch = [&](int e0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = e0 + EU * (64 * u + lane);
+            wv[u] = e < n ? *(const u32x4*)(wr + (T == GG_F32 ? 4 : 2) * e) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    const int nu = n / 64;
+    if constexpr (T == GG_Q4_K) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int u = min(64 * k + lane, nu - 1);  // loads stay in the row; the sum skips it
+            const uint8_t* blk = wr + 144 * (u >> 2);
+            wv[3 * k] = *(const u32x4*)blk;
+            wv[3 * k + 1] = *(const u32x4*)(blk + 16 + 32 * (u & 3));
+            wv[3 * k + 2] = *(const u32x4*)(blk + 32 + 32 * (u & 3));
+        }
+    } else {
+        load_batch(0);
+    }
+    // Q4_K: lane u reads x[64 u, 64 u + 64); in LDS every 64 floats are
+    // followed by 4 of padding, so the lanes' 16-byte reads fall on different
+    // banks (unpadded, all 64 lanes hit the same four banks)
+    auto xp = [&](int e) __attribute__((always_inline)) { return T == GG_Q4_K ? e + 4 * (e >> 6) : e; };
+    {  // x to LDS while the weights load: every load of the thread issued before its stores
+        constexpr int XPT = PQA_MAX_EMBD / (64 * kProjWaves);
+        float xv[XPT];
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int i = tid + 64 * kProjWaves * k;
+            xv[k] = i < n ? x[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const int i = tid + 64 * kProjWaves * k;
+            if (i < n) xs[xp(i)] = xv[k];
+        }
+    }
+    __syncthreads();
+    float* xg = xs + xp(n);  // Q4_K: the sum of each 32-element group of x, shared by every row
+    if constexpr (T == GG_Q4_K) {
+        if (tid < n / 32) {
+            float sg = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const floatx4 v4 = *(const floatx4*)(xs + xp(32 * tid) + 4 * i);
+                sg = sg + ((v4[0] + v4[1]) + (v4[2] + v4[3]));
+            }
+            xg[tid] = sg;
+        }
+        __syncthreads();
+    }
+    if (row >= m.rows) return;
+    float acc = 0.0f;
+    if constexpr (T == GG_F32 || T == GG_F16) {
+        for (int e0 = 0; e0 < n; e0 += 64 * EU * 8) {
+            if (e0) load_batch(e0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int e = e0 + EU * (64 * u + lane);
+                if (e < n) {
+                    if constexpr (T == GG_F32) {
+                        const floatx4 xq = *(const floatx4*)(xs + e);
+#pragma unroll
+                        for (int b = 0; b < 4; b++) acc = fmaf(__uint_as_float(wv[u][b]), xq[b], acc);
+                    } else {
+                        const floatx4 xa = *(const floatx4*)(xs + e), xb = *(const floatx4*)(xs + e + 4);
+#pragma unroll
+                        for (int b = 0; b < 4; b++) {
+                            const float xl = b < 2 ? xa[2 * b] : xb[2 * b - 4];
+                            const float xh = b < 2 ? xa[2 * b + 1] : xb[2 * b - 3];
+                            acc = fmaf(h2f(wv[u][b] & 0xFFFF), xl, acc);
+                            acc = fmaf(h2f(wv[u][b] >> 16), xh, acc);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int u = 64 * k + lane;
+            if (u < nu) {
+                const u32x4 hdr = wv[3 * k], qa = wv[3 * k + 1], qb = wv[3 * k + 2];
+                const int jj = u & 3;
+                const float* xu = xs + xp(64 * u);
+                const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+                unsigned sc, mn;
+                scale_min_k4_regs(2 * jj, hdr.y, hdr.z, hdr.w, sc, mn);
+                const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+                scale_min_k4_regs(2 * jj + 1, hdr.y, hdr.z, hdr.w, sc, mn);
+                const float d2 = d * (float)sc, m2 = dmin * (float)mn;
+                // sum over a group of (d q - m) x = d sum q x - m sum x: per
+                // element one nibble, one conversion and one fused product
+                const unsigned q8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const floatx4 xl = *(const floatx4*)(xu + 4 * i), xh = *(const floatx4*)(xu + 32 + 4 * i);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const unsigned byte = (q8[i] >> (8 * b)) & 0xFF;
+                        s1 = fmaf((float)(byte & 0xF), xl[b], s1);
+                        s2 = fmaf((float)(byte >> 4), xh[b], s2);
+                    }
+                }
+                acc = fmaf(d1, s1, acc);
+                acc = fmaf(-m1, xg[2 * u], acc);
+                acc = fmaf(d2, s2, acc);
+                acc = fmaf(-m2, xg[2 * u + 1], acc);
+            }
+        }
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) {
+        if (m.b) acc = acc + (m.btype == GG_F32 ? ((const float*)m.b)[row] : h2f(ld16(m.b + 2 * row)));
+        m.out[row] = m.add_out ? m.out[row] + acc : acc;
+    }
+}
+
 // LDS: x [n] floats, the raw chunk ring (kProjSlots x 8 x kProjChunkMax
 // bytes) and two product buffers (64 x kPS floats each).
 __host__ __device__ inline size_t proj_x_bytes(int n) { return ((size_t)n * 4 + 15) / 16 * 16; }
@@ -341,6 +493,15 @@ __global__ __launch_bounds__(64 * kProjWaves) void proj_kernel(const ProjArgs a)
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.m[mi + 1].wg0) mi++;
     const ProjMat& m = a.m[mi];
     const int lwg = (int)blockIdx.x - m.wg0;
+    if (m.fast) {
+        switch (m.wtype) {
+            case GG_F32: gemv_wg<GG_F32>(m, a.x, xs, a.n, lwg); break;
+            case GG_F16: gemv_wg<GG_F16>(m, a.x, xs, a.n, lwg); break;
+            case GG_Q4_K: gemv_wg<GG_Q4_K>(m, a.x, xs, a.n, lwg); break;
+            default: break;
+        }
+        return;
+    }
     switch (m.wtype) {
         case GG_F32: proj_wg<GG_F32>(m, a.x, xs, ring, prod, a.n, lwg); break;
         case GG_F16: proj_wg<GG_F16>(m, a.x, xs, ring, prod, a.n, lwg); break;
@@ -353,6 +514,10 @@ __global__ __launch_bounds__(64 * kProjWaves) void proj_kernel(const ProjArgs a)
 }
 
 size_t proj_lds_bytes(int n) { return proj_x_bytes(n) + kProjFixedLds; }
+// the any-order q rows use the front of the same allocation: x with 4 floats
+// of padding per 64 and one sum per 32-element group
+static_assert((PQA_MAX_EMBD + PQA_MAX_EMBD / 16 + PQA_MAX_EMBD / 32) * 4 <= PQA_MAX_EMBD * 4 + kProjFixedLds,
+              "padded x and group sums exceed the projection LDS");
 
 }  // namespace pqa
 
@@ -526,18 +691,25 @@ hipError_t launch_qkv_project(pqa_ctx* ctx, int layer, const float* xb, float* q
     ProjArgs a;
     float* outs[3] = {q, k, v};
     const int rows[3] = {(int)ctx->q_dim, (int)ctx->kv_dim, (int)ctx->kv_dim};
+    // q on the any-order rows when its type has them: its workgroups (one row
+    // per wave) come after K's and V's, which keep the reference's order and
+    // take longer, so both kinds share the CUs in one round
+    const bool fast_q = !ctx->token_exact_q && gemv_type(p.wtype[0]);
+    const int order[3] = {fast_q ? 1 : 0, fast_q ? 2 : 1, fast_q ? 0 : 2};
     int wgs = 0;
-    for (int i = 0; i < 3; i++) {
-        a.m[i].w = (const uint8_t*)p.w[i];
-        a.m[i].b = (const uint8_t*)p.b[i];
-        a.m[i].out = outs[i];
-        a.m[i].add_out = 0;
-        a.m[i].rows = rows[i];
-        a.m[i].wtype = p.wtype[i];
-        a.m[i].btype = p.btype[i];
-        a.m[i].stride = p.stride[i];
-        a.m[i].wg0 = wgs;
-        wgs += (rows[i] + kProjRows - 1) / kProjRows;
+    for (int j = 0; j < 3; j++) {
+        const int i = order[j];
+        a.m[j].w = (const uint8_t*)p.w[i];
+        a.m[j].b = (const uint8_t*)p.b[i];
+        a.m[j].out = outs[i];
+        a.m[j].add_out = 0;
+        a.m[j].rows = rows[i];
+        a.m[j].wtype = p.wtype[i];
+        a.m[j].btype = p.btype[i];
+        a.m[j].stride = p.stride[i];
+        a.m[j].wg0 = wgs;
+        a.m[j].fast = i == 0 && fast_q;
+        wgs += a.m[j].fast ? (rows[i] + kProjWaves - 1) / kProjWaves : (rows[i] + kProjRows - 1) / kProjRows;
     }
     a.x = xb;
     a.n = p.n_embd;
@@ -558,6 +730,7 @@ hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float*
     a.m[0].btype = p.btype[3];
     a.m[0].stride = p.stride[3];
     a.m[0].wg0 = 0;
+    a.m[0].fast = 0;
     a.x = attn;
     a.n = (int)ctx->q_dim;
     a.nmat = 1;
@@ -573,6 +746,13 @@ static int check_proj(pqa_ctx* ctx, int layer, const char* fn) {
     if (layer < 0 || layer >= ctx->n_layers) return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": bad layer");
     if (ctx->proj.empty() || !ctx->proj[layer].n_embd)
         return set_err(ctx, PQA_ERR_ARG, std::string(fn) + ": no projection weights for this layer");
+    return PQA_OK;
+}
+
+extern "C" int pqa_set_token_projection(pqa_ctx* ctx, int exact_q) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_token_projection: ctx is NULL");
+    if (exact_q != 0 && exact_q != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_token_projection: exact_q must be 0 or 1");
+    ctx->token_exact_q = exact_q;
     return PQA_OK;
 }
 

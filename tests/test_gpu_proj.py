@@ -1,9 +1,11 @@
 """Q/K/V projections on the GPU (pqa_qkv_project, pqa_decode_x through
 libpqa.so) against the projection oracle, which is bit-equal to the
-reference's matmul_bias: q, k and v bit-exact for every weight type, with and
-without biases, at small shapes and at the Qwen3-8B layer shape; the attention
-block from xb (pqa_decode_x) with its appended K/V rows bit-exact and its
-output within max-abs 2e-3 / rel 1e-2 of the oracle."""
+reference's matmul_bias: k and v bit-exact for every weight type, with and
+without biases, at small shapes and at the Qwen3-8B layer shape; q bit-exact
+with pqa_set_token_projection(1) and, by default, within the fp32 reordering
+bound for the types of the any-order path (F32, F16, Q4_K) and bit-exact for
+the others; the attention block from xb (pqa_decode_x) with its appended K/V
+rows bit-exact and its output within max-abs 2e-3 / rel 1e-2 of the oracle."""
 import ctypes as C
 
 import numpy as np
@@ -27,9 +29,61 @@ def _project(att, layer, x):
     return q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
 
 
-def _check(att, layer, x, mats):
+FAST_Q = (O.GGUF_F32, O.GGUF_F16, O.GGUF_Q4_K)  # q types of the any-order path
+
+
+def _q4k_term_magnitudes(raw, n):
+    """|d q| + |m| per element of Q4_K rows (w = d q - m, cpp/quant.hpp:210-236):
+    the any-order path sums d sum q x - m sum x per 32-element group."""
+    rows = raw.shape[0]
+    blk = raw.reshape(rows, n // 256, 144)
+    d = blk[:, :, 0:2].copy().view("<f2")[..., 0].astype(np.float32)
+    dmin = blk[:, :, 2:4].copy().view("<f2")[..., 0].astype(np.float32)
+    sc = blk[:, :, 4:16].astype(np.int64)
+    qs = blk[:, :, 16:144].astype(np.int64)
+    out = np.zeros((rows, n // 256, 256), np.float64)
+    for j in range(8):
+        if j < 4:
+            s_, m_ = sc[..., j] & 63, sc[..., j + 4] & 63
+        else:
+            s_ = (sc[..., j + 4] & 0xF) | ((sc[..., j - 4] >> 6) << 4)
+            m_ = (sc[..., j + 4] >> 4) | ((sc[..., j] >> 6) << 4)
+        d1 = (d * s_.astype(np.float32)).astype(np.float64)
+        m1 = (dmin * m_.astype(np.float32)).astype(np.float64)
+        jj, hi = j // 2, j % 2
+        q = (qs[..., 32 * jj:32 * jj + 32] >> (4 * hi)) & 0xF
+        out[..., 64 * jj + 32 * hi:64 * jj + 32 * hi + 32] = np.abs(d1[..., None] * q) + np.abs(m1[..., None])
+    return out.reshape(rows, n)
+
+
+def _q_within_reordering_bound(g, x, w, wt, rows, b, bt):
+    # any summation order over n fused products, then the bias: at most
+    # (n + 12) 2^-24 (sum_i |w_i x_i| + |b|) from the reference's sum (F32 and
+    # F16 weights enter as they are); Q4_K groups are summed as d sum q x -
+    # m sum x, so their terms are |d q_i| and |m| instead of |w_i|
+    n = x.shape[0]
+    want = O.matmul_bias(x, w, wt, rows, b, bt).astype(np.float64)
+    if wt == O.GGUF_Q4_K:
+        wf = _q4k_term_magnitudes(w, n)
+    else:
+        wf = np.stack([O.dequant_row(wt, w[r], n) for r in range(rows)]).astype(np.float64)
+    mag = np.abs(wf) @ np.abs(x.astype(np.float64))
+    if b is not None:
+        bias = b.view(np.float16) if bt == O.GGUF_F16 else b.view(np.float32)
+        mag = mag + np.abs(bias.astype(np.float64))
+    err = np.abs(g.astype(np.float64) - want)
+    bound = (n + 12) * 2.0 ** -24 * mag + 1e-30
+    assert np.all(err <= bound), (wt, float(np.max(err / bound)))
+    # and in practice far inside it: a few ulps of sum |w x|
+    assert float(np.median(err / (mag + 1e-30))) < 16 * 2.0 ** -24, wt
+
+
+def _check(att, layer, x, mats, exact_q=False):
     got = _project(att, layer, x)
     for name, g, (w, wt, rows, b, bt) in zip("qkv", got, mats):
+        if name == "q" and not exact_q and wt in FAST_Q:
+            _q_within_reordering_bound(g, x, w, wt, rows, b, bt)
+            continue
         want = O.matmul_bias(x, w, wt, rows, b, bt)
         assert_bits_equal(g.view(np.uint32), want.view(np.uint32), f"{name} (type {wt}, bias {bt})")
 
@@ -49,6 +103,10 @@ def test_projection_bit_exact_per_type(wtype, n):
     att.set_qkv_weights(0, n, wq, wtype, wk, wtype, wv, wtype, bq, bqt, bk, bkt, bv, bvt)
     x = rng.standard_normal(n).astype(np.float32)
     _check(att, 0, x, mats)
+    att.set_token_projection(True)
+    _check(att, 0, x, mats, exact_q=True)
+    att.set_token_projection(False)
+    _check(att, 0, x, mats)
     att.close()
 
 
@@ -65,6 +123,29 @@ def test_projection_qwen3_8b_layer_mixed_types():
     for seed in range(2):
         x = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
         _check(att, 1, x, mats)
+    att.set_token_projection(True)
+    _check(att, 1, x, mats, exact_q=True)
+    att.close()
+
+
+@pytest.mark.parametrize("wtype,n", [(O.GGUF_F32, 8192), (O.GGUF_F16, 8192), (O.GGUF_Q4_K, 8192), (O.GGUF_F32, 520),
+                                     (O.GGUF_F16, 2056), (O.GGUF_Q4_K, 2560)])
+def test_any_order_q_widths(wtype, n):
+    # the any-order q rows at the widest input (8192: several batches of
+    # units per lane) and at widths that leave lanes without a unit (F32 520,
+    # F16 2056: a partial batch; Q4_K 2560: 40 quarter blocks for 64 lanes);
+    # 300 q rows, so the last workgroup has waves past the last row
+    print(f"any-order q type {wtype} n {n}", flush=True)
+    rng = np.random.default_rng(4000 + n + wtype)
+    att = PicoAttention(1, 16, 3, 1, 100)
+    q_rows, kv_rows = 300, 100
+    mats = [(make_rows(rng, wtype, q_rows, n), wtype, q_rows, make_bias(rng, O.GGUF_F16, q_rows), O.GGUF_F16),
+            (make_rows(rng, wtype, kv_rows, n), wtype, kv_rows, None, O.GGUF_NONE),
+            (make_rows(rng, wtype, kv_rows, n), wtype, kv_rows, make_bias(rng, O.GGUF_F32, kv_rows), O.GGUF_F32)]
+    att.set_qkv_weights(0, n, mats[0][0], wtype, mats[1][0], wtype, mats[2][0], wtype,
+                        mats[0][3], O.GGUF_F16, None, 0, mats[2][3], O.GGUF_F32)
+    x = rng.standard_normal(n).astype(np.float32)
+    _check(att, 0, x, mats)
     att.close()
 
 
