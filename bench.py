@@ -769,6 +769,10 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
 
     _, oev = timed(torch, cx, ostep, steps, warmup)
     ous = oev * 1e3 / n_layers
+    cx.check(cx.L.pqa_set_out_projection(cx.h, 0), cx.h)  # the opt-in any-order rows
+    _, oev_any = timed(torch, cx, ostep, steps, warmup)
+    cx.check(cx.L.pqa_set_out_projection(cx.h, 1), cx.h)
+    ous_any = oev_any * 1e3 / n_layers
     res = {"workload": "qwen3_8b_qkv_proj_q4_k_m", "n_embd": n, "rows": [nh * hd, nkv * hd, nkv * hd],
            "weight_types": ["Q4_K", "Q4_K", "Q6_K"], "weight_bytes_per_layer": wbytes,
            "us_per_layer": round(us, 3), "weight_GB_per_s": round(gbs, 1),
@@ -779,7 +783,9 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
                                    "note": "pqa_set_token_projection(1): q, k and v bit-identical to matmul_bias"},
            "out_proj": {"rows": n, "width": nh * hd, "weight_type": "Q4_K", "weight_bytes_per_layer": obytes,
                         "us_per_layer": round(ous, 3), "weight_GB_per_s": round(obytes / (ous * 1e-6) / 1e9, 1),
-                        "note": "attn_output matmul_bias + residual vec_add (cpp/model.hpp:420-427)"}}
+                        "any_order_us_per_layer": round(ous_any, 3),
+                        "note": "attn_output matmul_bias + residual vec_add (cpp/model.hpp:420-427), the reference's "
+                                "order (default); any_order: pqa_set_out_projection(0)"}}
     if cpu:
         import oracle as O
         if O.RefModel.available("B"):
@@ -808,7 +814,8 @@ def proj_workload(torch, dev, n_layers=36, nh=32, nkv=8, hd=128, n=4096, steps=2
                                    ref.matmul_bias(xh, w0[2], Q6K, nkv * hd).view(np.uint32)))
     cx.close()
     log(f"[bench] qkv projection: {us:.2f} us/layer, {gbs:.0f} GB/s of weights ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM); "
-        f"all in the reference's order {us_exact:.2f} us; {res.get('cpu_baseline')}")
+        f"all in the reference's order {us_exact:.2f} us; attn_output {ous:.2f} us (any order {ous_any:.2f} us); "
+        f"{res.get('cpu_baseline')}")
     return res
 
 

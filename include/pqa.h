@@ -228,6 +228,18 @@ int pqa_decode_x(pqa_ctx* ctx, int layer, int pos, const float* xb, float* out);
 int pqa_set_out_weights(pqa_ctx* ctx, int layer, int n_embd, const void* wo, int wo_type, const void* bo,
                         int bo_type);
 
+/* How pqa_out_project and pqa_attention_block (and its host form) sum the
+ * attn_output rows.
+ * 1 (default): the reference's order; x is bit-identical to matmul_bias then
+ *    vec_add.
+ * 0: rows of type F32, F16 or Q4_K on the any-order path of
+ *    pqa_set_token_projection (one row per wave), within (q_dim + 12) 2^-24
+ *    sum_i |w_i a_i| (Q4_K: |d q_i| + |m| in place of |w_i|) of the
+ *    reference's sum before the residual add; other types keep the order.
+ * No counterpart in the reference, which has one order only.
+ */
+int pqa_set_out_projection(pqa_ctx* ctx, int exact);
+
 /* x[n_embd] += Wo attn + bo, DEVICE pointers attn [q_dim] and x (updated in
  * place); asynchronous on the context stream. */
 int pqa_out_project(pqa_ctx* ctx, int layer, const float* attn, float* x);

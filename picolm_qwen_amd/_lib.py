@@ -22,7 +22,7 @@ EXPORTS = [
     "pqa_create", "pqa_set_qk_norm", "pqa_decode", "pqa_prefill", "pqa_decode_host",
     "pqa_prefill_host", "pqa_kv_upload", "pqa_kv_download", "pqa_kv_cache", "pqa_stream",
     "pqa_sync", "pqa_last_error", "pqa_destroy", "pqa_rope_table", "pqa_fp32_to_fp16",
-    "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_set_batch_projection", "pqa_set_token_projection", "pqa_kvc_save", "pqa_kvc_load",
+    "pqa_synth_kv", "pqa_set_decode_split", "pqa_set_prefill_precision", "pqa_set_batch_projection", "pqa_set_token_projection", "pqa_set_out_projection", "pqa_kvc_save", "pqa_kvc_load",
     "pqa_set_qkv_weights", "pqa_qkv_project", "pqa_decode_x", "pqa_set_out_weights", "pqa_out_project",
     "pqa_attention_block", "pqa_qkv_project_batch", "pqa_prefill_x", "pqa_decode_noalloc",
     "pqa_out_project_batch", "pqa_prefill_block", "pqa_attention_block_host", "pqa_prefill_block_host",
@@ -106,6 +106,7 @@ def _bind(L: C.CDLL) -> C.CDLL:
     L.pqa_set_prefill_precision.argtypes = [vp, i]
     L.pqa_set_batch_projection.argtypes = [vp, i]
     L.pqa_set_token_projection.argtypes = [vp, i]
+    L.pqa_set_out_projection.argtypes = [vp, i]
     L.pqa_kvc_save.argtypes = [vp, C.c_char_p, i]
     L.pqa_kvc_load.argtypes = [vp, C.c_char_p]
     L.pqa_set_qkv_weights.argtypes = [vp, i, i] + [vp, i, vp, i] * 3

@@ -224,6 +224,13 @@ class PicoAttention:
         reference's order either way."""
         check(lib().pqa_set_token_projection(self.handle, int(bool(exact_q))), self.handle)
 
+    def set_out_projection(self, exact: bool) -> None:
+        """True (the default): the one-token attn_output projection in the
+        reference's order (bit-identical x); False: its F32, F16 and Q4_K rows
+        in any order on the bandwidth-bound path (within the fp32 reordering
+        bound)."""
+        check(lib().pqa_set_out_projection(self.handle, int(bool(exact))), self.handle)
+
     # -- the block ----------------------------------------------------------
     def set_qk_norm(self, layer: int, q_norm_w, k_norm_w) -> None:
         """Layer's attn_q_norm / attn_k_norm weights ([head_dim] each); None turns it off."""

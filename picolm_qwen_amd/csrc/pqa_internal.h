@@ -71,6 +71,9 @@ struct pqa_ctx {
     // bandwidth-bound path, k and v in the reference's order; 1 all three in
     // the reference's order
     int token_exact_q = 0;
+    // attn_output of one token (pqa_out_project, pqa_attention_block): 1
+    // (default) the reference's order; 0 rows of F32, F16 and Q4_K in any order
+    int out_exact = 1;
 
     // batched projections: 1 (default) the K and V columns in the reference's
     // summation order (bit-exact cache rows), q on the split fp16 GEMM; 0 all

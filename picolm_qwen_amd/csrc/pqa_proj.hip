@@ -730,11 +730,12 @@ hipError_t launch_out_project(pqa_ctx* ctx, int layer, const float* attn, float*
     a.m[0].btype = p.btype[3];
     a.m[0].stride = p.stride[3];
     a.m[0].wg0 = 0;
-    a.m[0].fast = 0;
+    a.m[0].fast = !ctx->out_exact && gemv_type(p.wtype[3]);
     a.x = attn;
     a.n = (int)ctx->q_dim;
     a.nmat = 1;
-    hipLaunchKernelGGL(proj_kernel, dim3((p.out_rows + kProjRows - 1) / kProjRows), dim3(64 * kProjWaves),
+    const int rpw = a.m[0].fast ? kProjWaves : kProjRows;  // rows per workgroup
+    hipLaunchKernelGGL(proj_kernel, dim3((p.out_rows + rpw - 1) / rpw), dim3(64 * kProjWaves),
                        proj_lds_bytes(a.n), ctx->stream, a);
     return hipGetLastError();
 }
@@ -753,6 +754,13 @@ extern "C" int pqa_set_token_projection(pqa_ctx* ctx, int exact_q) {
     if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_token_projection: ctx is NULL");
     if (exact_q != 0 && exact_q != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_token_projection: exact_q must be 0 or 1");
     ctx->token_exact_q = exact_q;
+    return PQA_OK;
+}
+
+extern "C" int pqa_set_out_projection(pqa_ctx* ctx, int exact) {
+    if (!ctx) return set_err(nullptr, PQA_ERR_ARG, "pqa_set_out_projection: ctx is NULL");
+    if (exact != 0 && exact != 1) return set_err(ctx, PQA_ERR_ARG, "pqa_set_out_projection: exact must be 0 or 1");
+    ctx->out_exact = exact;
     return PQA_OK;
 }
 

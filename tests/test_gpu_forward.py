@@ -158,6 +158,38 @@ def test_host_entry_points_equal_device_ones(n_tok):
         a.close()
 
 
+def test_host_attention_block_equals_device_on_the_any_order_paths():
+    # Q4_K q and attn_output rows: the host entry takes the same any-order q
+    # path (the default) and, switched on, the any-order attn_output path, as
+    # the device entry: bit-equal x and cache rows
+    print("host attention block, any-order paths", flush=True)
+    rng = np.random.default_rng(4711)
+    nh, nkv, hd, dim, smax = 16, 4, 128, 2048, 64
+    types = (O.GGUF_Q4_K, O.GGUF_Q4_K, O.GGUF_Q6_K, O.GGUF_Q4_K)
+    w, b = _layer(rng, nh, nkv, hd, dim, types, bias=True)
+    cos, sin = O.rope_table(1e6, hd, smax)
+    host, dev = (PicoAttention(1, smax, nh, nkv, hd, 0, rope_cos=cos, rope_sin=sin) for _ in range(2))
+    for a in (host, dev):
+        _set(a, 0, dim, w, b, types)
+        a.synth_kv(0, 0, 20, 3, 0.0)
+    for pos, out_exact in ((20, True), (21, False)):
+        for a in (host, dev):
+            a.set_out_projection(out_exact)
+        xb1 = rng.standard_normal(dim).astype(np.float32)
+        x1 = rng.standard_normal(dim).astype(np.float32)
+        h1 = x1.copy()
+        host.attention_block(0, pos, xb1, h1)
+        d1 = torch.from_numpy(x1.copy()).to(DEV)
+        dev.attention_block(0, pos, torch.from_numpy(xb1).to(DEV), d1)
+        assert_bits_equal(h1.view(np.uint32), d1.cpu().numpy().view(np.uint32), f"x at {pos}")
+    hk, hv = host.kv_download(0, 0, 22)
+    dk, dv = dev.kv_download(0, 0, 22)
+    assert_bits_equal(hk, dk, "K rows")
+    assert_bits_equal(hv, dv, "V rows")
+    for a in (host, dev):
+        a.close()
+
+
 @pytest.mark.parametrize("qk_norm,bias", [(True, False), (False, True)])
 def test_compiled_adapter_runs_the_reference_loops(qk_norm, bias):
     # two layers, a 24-token prompt through forward_batch_layers, then 4 tokens

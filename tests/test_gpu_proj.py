@@ -273,6 +273,44 @@ def test_out_projection_with_residual_bit_exact(wtype, bt):
     att.close()
 
 
+@pytest.mark.parametrize("wtype,bt", [(O.GGUF_Q4_K, O.GGUF_NONE), (O.GGUF_F16, O.GGUF_F16), (O.GGUF_F32, O.GGUF_F32)])
+def test_out_projection_any_order_within_bound(wtype, bt):
+    # pqa_set_out_projection(0): x = x0 + (Wo attn + bo) with the sum in any
+    # order, within the reordering bound of the sum, plus the residual add's
+    # own rounding; then back to the reference's order, bit-exact again
+    print(f"out projection any order type {wtype}", flush=True)
+    rng = np.random.default_rng(720 + wtype)
+    nh, nkv, hd, dim = 32, 8, 128, 2560
+    att = PicoAttention(1, 16, nh, nkv, hd)
+    wo = make_rows(rng, wtype, dim, nh * hd)
+    bo = None if bt == O.GGUF_NONE else make_bias(rng, bt, dim)
+    att.set_out_weights(0, dim, wo, wtype, bo, bt)
+    dev = torch.device("cuda:0")
+    attn = rng.standard_normal(nh * hd).astype(np.float32)
+    x0 = rng.standard_normal(dim).astype(np.float32)
+    att.set_out_projection(False)
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.out_project(0, torch.from_numpy(attn).to(dev), x)
+    got = x.cpu().numpy().astype(np.float64)
+    want = (x0 + O.matmul_bias(attn, wo, wtype, dim, bo, bt)).astype(np.float32).astype(np.float64)
+    n = nh * hd
+    if wtype == O.GGUF_Q4_K:
+        wf = _q4k_term_magnitudes(wo, n)
+    else:
+        wf = np.stack([O.dequant_row(wtype, wo[r], n) for r in range(dim)]).astype(np.float64)
+    mag = np.abs(wf) @ np.abs(attn.astype(np.float64))
+    if bo is not None:
+        mag = mag + np.abs((bo.view(np.float16) if bt == O.GGUF_F16 else bo.view(np.float32)).astype(np.float64))
+    bound = (n + 12) * 2.0 ** -24 * mag + 2.0 ** -23 * np.abs(want) + 1e-30
+    err = np.abs(got - want)
+    assert np.all(err <= bound), float(np.max(err / bound))
+    att.set_out_projection(True)
+    x = torch.from_numpy(x0.copy()).to(dev)
+    att.out_project(0, torch.from_numpy(attn).to(dev), x)
+    assert_bits_equal(x.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32), "x, reference order")
+    att.close()
+
+
 def test_attention_block_from_xb_to_residual():
     # the whole attention half of a Qwen3-4B layer at pos 200: K/V rows
     # bit-exact, x within the output tolerance (it carries the attention output)
