@@ -7,7 +7,9 @@ never as a compute path of the product.
 
 Functions restated from the reference (rain1201/picolm_qwen) and the pin of
 each one (closed form, exhaustive KAT or golden vector) are listed in
-oracle/pqa_oracle.h.
+oracle/pqa_oracle.h. q4k_term_magnitudes (the per-element terms of the
+any-order Q4_K sums' error bound) is pinned by a closed-form block and by its
+limits against the dequantization (tests/test_oracle_proj.py).
 """
 from __future__ import annotations
 
@@ -307,6 +309,33 @@ def dequant_row(wtype, raw, n):
 def vec_dot(wtype, raw_row, x):
     x = np.ascontiguousarray(x, np.float32)
     return float(lib().pqo_vec_dot(wtype, _vp(np.ascontiguousarray(raw_row)), x, x.size))
+
+
+def q4k_term_magnitudes(raw, n):
+    """|d q| + |m| per element of Q4_K rows [rows][row bytes] of n elements,
+    float64 [rows][n]: w = d q - m with d = d_super * sc and m = dmin * mn of
+    the element's 32-element group (get_scale_min_k4 and dequantize_row_q4_K,
+    cpp/quant.hpp:210-236). The terms a sum in the form d sum q x - m sum x
+    rounds, for its error bound."""
+    rows = raw.shape[0]
+    blk = np.ascontiguousarray(raw).reshape(rows, n // 256, 144)
+    d = blk[:, :, 0:2].copy().view("<f2")[..., 0].astype(np.float32)
+    dmin = blk[:, :, 2:4].copy().view("<f2")[..., 0].astype(np.float32)
+    sc = blk[:, :, 4:16].astype(np.int64)
+    qs = blk[:, :, 16:144].astype(np.int64)
+    out = np.zeros((rows, n // 256, 256), np.float64)
+    for j in range(8):
+        if j < 4:
+            s_, m_ = sc[..., j] & 63, sc[..., j + 4] & 63
+        else:
+            s_ = (sc[..., j + 4] & 0xF) | ((sc[..., j - 4] >> 6) << 4)
+            m_ = (sc[..., j + 4] >> 4) | ((sc[..., j] >> 6) << 4)
+        d1 = (d * s_.astype(np.float32)).astype(np.float64)
+        m1 = (dmin * m_.astype(np.float32)).astype(np.float64)
+        jj, hi = j // 2, j % 2
+        q = (qs[..., 32 * jj:32 * jj + 32] >> (4 * hi)) & 0xF
+        out[..., 64 * jj + 32 * hi:64 * jj + 32 * hi + 32] = np.abs(d1[..., None] * q) + np.abs(m1[..., None])
+    return out.reshape(rows, n)
 
 
 def matmul_bias(x, w_raw, wtype, d, b_raw=None, btype=GGUF_NONE):

@@ -32,30 +32,6 @@ def _project(att, layer, x):
 FAST_Q = (O.GGUF_F32, O.GGUF_F16, O.GGUF_Q4_K)  # q types of the any-order path
 
 
-def _q4k_term_magnitudes(raw, n):
-    """|d q| + |m| per element of Q4_K rows (w = d q - m, cpp/quant.hpp:210-236):
-    the any-order path sums d sum q x - m sum x per 32-element group."""
-    rows = raw.shape[0]
-    blk = raw.reshape(rows, n // 256, 144)
-    d = blk[:, :, 0:2].copy().view("<f2")[..., 0].astype(np.float32)
-    dmin = blk[:, :, 2:4].copy().view("<f2")[..., 0].astype(np.float32)
-    sc = blk[:, :, 4:16].astype(np.int64)
-    qs = blk[:, :, 16:144].astype(np.int64)
-    out = np.zeros((rows, n // 256, 256), np.float64)
-    for j in range(8):
-        if j < 4:
-            s_, m_ = sc[..., j] & 63, sc[..., j + 4] & 63
-        else:
-            s_ = (sc[..., j + 4] & 0xF) | ((sc[..., j - 4] >> 6) << 4)
-            m_ = (sc[..., j + 4] >> 4) | ((sc[..., j] >> 6) << 4)
-        d1 = (d * s_.astype(np.float32)).astype(np.float64)
-        m1 = (dmin * m_.astype(np.float32)).astype(np.float64)
-        jj, hi = j // 2, j % 2
-        q = (qs[..., 32 * jj:32 * jj + 32] >> (4 * hi)) & 0xF
-        out[..., 64 * jj + 32 * hi:64 * jj + 32 * hi + 32] = np.abs(d1[..., None] * q) + np.abs(m1[..., None])
-    return out.reshape(rows, n)
-
-
 def _q_within_reordering_bound(g, x, w, wt, rows, b, bt):
     # any summation order over n fused products, then the bias: at most
     # (n + 12) 2^-24 (sum_i |w_i x_i| + |b|) from the reference's sum (F32 and
@@ -64,7 +40,7 @@ def _q_within_reordering_bound(g, x, w, wt, rows, b, bt):
     n = x.shape[0]
     want = O.matmul_bias(x, w, wt, rows, b, bt).astype(np.float64)
     if wt == O.GGUF_Q4_K:
-        wf = _q4k_term_magnitudes(w, n)
+        wf = O.q4k_term_magnitudes(w, n)
     else:
         wf = np.stack([O.dequant_row(wt, w[r], n) for r in range(rows)]).astype(np.float64)
     mag = np.abs(wf) @ np.abs(x.astype(np.float64))
@@ -125,6 +101,24 @@ def test_projection_qwen3_8b_layer_mixed_types():
         _check(att, 1, x, mats)
     att.set_token_projection(True)
     _check(att, 1, x, mats, exact_q=True)
+    att.close()
+
+
+@pytest.mark.parametrize("wtype,n", [(O.GGUF_F32, 8), (O.GGUF_F16, 8), (O.GGUF_Q4_K, 256)])
+def test_any_order_q_narrowest_rows(wtype, n):
+    # the narrowest rows each type allows (one F32 / F16 unit for two lanes,
+    # one Q4_K super-block: 4 of the wave's 64 lanes hold a unit) and a single
+    # q row, k and v rows of one head
+    print(f"any-order q narrow type {wtype} n {n}", flush=True)
+    rng = np.random.default_rng(5000 + n + wtype)
+    att = PicoAttention(1, 16, 1, 1, 64)
+    mats = [(make_rows(rng, wtype, 64, n), wtype, 64, make_bias(rng, O.GGUF_F32, 64), O.GGUF_F32),
+            (make_rows(rng, wtype, 64, n), wtype, 64, None, O.GGUF_NONE),
+            (make_rows(rng, wtype, 64, n), wtype, 64, None, O.GGUF_NONE)]
+    att.set_qkv_weights(0, n, mats[0][0], wtype, mats[1][0], wtype, mats[2][0], wtype, mats[0][3], O.GGUF_F32)
+    for seed in range(3):
+        x = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+        _check(att, 0, x, mats)
     att.close()
 
 
@@ -295,7 +289,7 @@ def test_out_projection_any_order_within_bound(wtype, bt):
     want = (x0 + O.matmul_bias(attn, wo, wtype, dim, bo, bt)).astype(np.float32).astype(np.float64)
     n = nh * hd
     if wtype == O.GGUF_Q4_K:
-        wf = _q4k_term_magnitudes(wo, n)
+        wf = O.q4k_term_magnitudes(wo, n)
     else:
         wf = np.stack([O.dequant_row(wtype, wo[r], n) for r in range(dim)]).astype(np.float64)
     mag = np.abs(wf) @ np.abs(attn.astype(np.float64))

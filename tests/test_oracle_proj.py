@@ -93,6 +93,40 @@ def test_closed_form_q4_k():
     assert np.array_equal(y, want)
 
 
+def test_q4k_term_magnitudes_closed_form_and_limits():
+    # the closed-form block above: |d q| + |m| = (j+1) q + j for sub-block j
+    sc = [j + 1 for j in range(8)]
+    mn = [2 * j for j in range(8)]
+    s12 = np.zeros(12, np.uint8)
+    for j in range(4):
+        s12[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        s12[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        s12[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    q = np.arange(256) % 16
+    qs = np.zeros(128, np.uint8)
+    for jj in range(4):
+        lo, hi = q[64 * jj:64 * jj + 32], q[64 * jj + 32:64 * jj + 64]
+        qs[32 * jj:32 * jj + 32] = lo | (hi << 4)
+    blk = np.concatenate([f16(1.0), f16(0.5), s12, qs])
+    got = O.q4k_term_magnitudes(blk[None, :], 256)[0]
+    want = np.array([sc[e // 32] * q[e] + 0.5 * mn[e // 32] for e in range(256)], np.float64)
+    assert np.array_equal(got, want)
+    # random rows against the dequantization: |d q| + |m| >= |w|; equal to |w|
+    # when d = 0 (w = -m) and, up to w's fp32 rounding, when dmin = 0 (w = d q)
+    rng = np.random.default_rng(77)
+    n = 512
+    raw = make_rows(rng, O.GGUF_Q4_K, 6, n).reshape(6, n // 256, 144).copy()
+    raw[0:2, :, 0:2] = 0   # d = +0
+    raw[2:4, :, 2:4] = 0   # dmin = +0
+    raw = raw.reshape(6, -1)
+    mag = O.q4k_term_magnitudes(raw, n)
+    w = np.abs(np.stack([O.dequant_row(O.GGUF_Q4_K, raw[r], n) for r in range(6)]).astype(np.float64))
+    assert np.array_equal(mag[0:2], w[0:2])
+    assert np.all(np.abs(mag[2:4] - w[2:4]) <= 2.0 ** -24 * w[2:4])
+    assert np.all(mag >= w * (1 - 2.0 ** -24))
+    assert np.any(mag[4:] > 1.5 * w[4:])  # the general rows do carry cancelling terms
+
+
 def test_closed_form_q6_k():
     # d = 1, scales s_i = i - 8; 6-bit q from the low/high planes, y = s * (q - 32)
     q6 = (np.arange(256) * 7) % 64
