@@ -61,6 +61,9 @@ def test_null_context_calls_fail_cleanly():
     assert L.pqa_sync(None) == _lib.PQA_ERR_ARG
     assert L.pqa_kvc_save(None, b"/nonexistent/x.kvc", 1) == _lib.PQA_ERR_ARG
     assert L.pqa_kvc_load(None, b"/nonexistent/x.kvc") == 0
+    for setter in (L.pqa_set_token_projection, L.pqa_set_out_projection, L.pqa_set_batch_projection,
+                   L.pqa_set_prefill_precision):
+        assert setter(None, 1) == _lib.PQA_ERR_ARG
     assert b"ctx is NULL" in L.pqa_last_error(None)
     assert L.pqa_stream(None) is None
     L.pqa_destroy(None)

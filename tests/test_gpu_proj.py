@@ -179,6 +179,9 @@ def test_rejected_shapes_and_types():
     p = [C.c_void_p(t.data_ptr()) for t in (xb, out, out, out)]
     assert _lib.lib().pqa_qkv_project(att.handle, 0, *p) == PQA_ERR_ARG
     assert "no projection weights" in att.last_error()
+    for setter, name in ((_lib.lib().pqa_set_token_projection, "exact_q"), (_lib.lib().pqa_set_out_projection, "exact")):
+        assert setter(att.handle, 2) == PQA_ERR_ARG and name in att.last_error()
+        assert setter(att.handle, 0) == 0 and setter(att.handle, 1) == 0
     att.close()
 
 
