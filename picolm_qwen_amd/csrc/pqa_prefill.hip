@@ -6,7 +6,9 @@
 //    token's position and the reference's fp16 rounding; V the rounding
 //    only. Rows start..start+n-1 of the layer slice are written.
 // 2. prefill_attn: flash attention over the fp16 cache on
-//    v_mfma_f32_32x32x16_f16. The query heads of one KV head are packed as
+//    v_mfma_f32_16x16x32_f16 (on this GPU a stream of them moves 20 % more
+//    MACs per second than v_mfma_f32_32x32x16_f16, with the same operand
+//    traffic per tile). The query heads of one KV head are packed as
 //    rows R = token*g + h (g = query heads per KV head), so one K/V tile in
 //    LDS serves the whole GQA group. A workgroup of 8 waves takes a pair of
 //    128-row blocks one after the other (a long and a short one, so every
@@ -16,8 +18,9 @@
 //    Per block: q rows are normed, rotated, scaled and rounded to fp16 into
 //    LDS (each lane holds whole RoPE pairs of its row, so the rotation needs
 //    no exchange). Per 64-key tile each wave computes S^T = K Q^T (keys x
-//    rows), the online softmax per row (a lane owns one row: its 32 scores
-//    plus the partner lane 32 apart), and O^T += V^T P^T. With S^T in the
+//    rows) in 16x16 blocks, the online softmax per row (a lane holds 16
+//    scores of each of two rows; a row's 64 scores sit in 4 lanes 16 apart),
+//    and O^T += V^T P^T. With S^T in the
 //    MFMA result layout the lane's scores are already the B operand of the
 //    PV product, so P never leaves registers. The running maximum is raised
 //    (and O, l rescaled) only when a score exceeds it by more than 2^8, so
@@ -256,19 +259,23 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: P stays <= 256 between res
 // 16-byte chunks of row r stored at chunk index c ^ swz(r). The direct
 // global->LDS loads pick, for each lane, the global chunk whose swizzled slot
 // is the lane's LDS slot, so the tile is written already swizzled.
-//   K: swz(r) = r mod chunks: the A-operand reads (32 rows, one chunk
-//      column) hit 16 distinct chunk slots per 16 lanes.
-//   V: swz(r) = 4 * (r mod 4): the transposed reads (8 rows x 4 chunks per
-//      instruction) touch every chunk slot exactly twice (the 2-pass minimum).
+//   K: swz(r) = r mod chunks: the A-operand reads (16 rows x 4 chunk
+//      columns per instruction) use every 16-byte bank slot 4 times, the
+//      minimum for 1 KB.
+//   V: swz(r) = 2 ((r / rows per 256 bytes) mod (chunks / 2)): the
+//      transposing reads (16 rows x one 32-byte dim block per instruction)
+//      use every 8-byte bank slot twice, the minimum for 512 bytes.
 template <int HD>
 struct PrefillTile {
+    static_assert(HD == 64 || HD == 128, "head sizes of the MFMA prefill");
     static constexpr int CH = HD / 8;            // 16-byte chunks per row
     static constexpr int ROWB = HD * 2;          // bytes per row
+    static constexpr int RPB = 256 / ROWB;       // rows per 256-byte bank window
     static constexpr int BYTES = kKeysPerTile * ROWB;
     static constexpr int RPI = 1024 / ROWB;      // rows per 1 KB wave-wide load
     static constexpr int NI = BYTES / 1024 / kGroupWaves;  // loads per wave per tile and operand
     __device__ static int swz_k(int r) { return r & (CH - 1); }
-    __device__ static int swz_v(int r) { return (4 * (r & 3)) & (CH - 1); }
+    __device__ static int swz_v(int r) { return 2 * ((r / RPB) & (CH / 2 - 1)); }
 };
 
 // SPLITQ: scores use q = hi + lo (two fp16 MFMAs into one fp32 accumulator),
@@ -276,8 +283,8 @@ struct PrefillTile {
 template <int HD, bool SPLITQ, bool YS>
 __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const AttnArgs a) {
     using T = PrefillTile<HD>;
-    constexpr int QK = HD / 16;  // k-steps of S^T = K Q^T
-    constexpr int DT = HD / 32;  // 32-dim tiles of O^T
+    constexpr int KS = HD / 32;  // 32-dim k-steps of S^T = K Q^T
+    constexpr int DB = HD / 16;  // 16-dim blocks of O^T
     constexpr float NEG_INF = -__builtin_huge_valf();
     __shared__ __attribute__((aligned(1024))) char lds[2][2][2][T::BYTES];  // [buffer][tile parity][K, V]
 
@@ -315,8 +322,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         int lane_j = tid & 63;
         asm volatile("" : "+v"(lane_j));
         const int lane = lane_j;
-        const int col = lane & 31;
-        const int hk = lane >> 5;
+        const int col = lane & 31;  // the lane's row in the output staging
+        // v_mfma_f32_16x16x32_f16 lane layout: A row / B column / D column
+        // c16, k elements 8 g16 .. +7, D rows 4 g16 .. +3
+        const int c16 = lane & 15, g16 = lane >> 4;
 
         // ---- per-lane offsets, fixed for the block's tile loop ----
         // global -> LDS: the waves of group par load tile 2 step + par; wave load i
@@ -330,27 +339,34 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             gk[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_k(r));
             gv[i] = (unsigned)(r * rowb) + 16u * (unsigned)(p ^ T::swz_v(r));
         }
-        // K fragment reads: row 32 t2 + col, chunk (2 ks + hk) ^ swz_k(col)
-        int koff[QK];
+        // K fragment of key block kb, k-step ks: row 16 kb + c16, chunk
+        // (4 ks + g16) ^ swz_k(row), and swz_k(16 kb + c16) = swz_k(c16)
+        int koff[KS];
 #pragma unroll
-        for (int ks = 0; ks < QK; ks++) koff[ks] = col * T::ROWB + 16 * ((2 * ks + hk) ^ T::swz_k(col));
-        // V^T fragment reads (transposing): row 16 s + 8 t + 4 hk + tr_e,
-        // dims 32 dt + 16 (g16 & 1) + 4 tr_q .. +3
-        const int j16 = lane & 15, g16 = lane >> 4;
-        const int tr_e = j16 >> 2, tr_q = j16 & 3;
-        int voff[DT];
+        for (int ks = 0; ks < KS; ks++) koff[ks] = c16 * T::ROWB + 16 * ((4 * ks + g16) ^ T::swz_k(c16));
+        // V^T fragment of dim block db, keys 32 s + [0, 32): two transposing
+        // reads (t = 0, 1). In each 16-lane group the lane gives key row
+        // 32 s + 16 t + 4 g16 + c16 / 4, dims 16 db + 4 (c16 % 4) .. +3, and
+        // receives dim 16 db + c16 of the group's 4 keys: k elements 8 g16 + 4 t
+        // .. +3 are keys 32 s + 16 t + 4 g16 .. +3, the keys the lane's scores
+        // hold (see the P layout below). swz_v of the row depends on 4 g16 +
+        // c16 / 4 only.
+        const int vr0 = 4 * g16 + (c16 >> 2);
+        int voff[DB];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int c = 4 * dt + 2 * (g16 & 1) + (tr_q >> 1);
-            voff[dt] = (4 * hk + tr_e) * T::ROWB + 16 * (c ^ T::swz_v(tr_e)) + 8 * (tr_q & 1);
-        }
+        for (int db = 0; db < DB; db++)
+            voff[db] = vr0 * T::ROWB + 16 * ((2 * db + ((c16 & 3) >> 1)) ^ T::swz_v(vr0)) + 8 * (c16 & 1);
 
         const int R0 = b * kRowsPerBlock + wr * 32;
         const int R = R0 + col;
         const bool rvalid = R < a.rows;
         const int tok = rvalid ? R / a.g : 0;
         const int hq = kvh * a.g + (rvalid ? R - (R / a.g) * a.g : 0);
-        const int qpos = a.start + tok;
+        // positions of the lane's two score rows R0 + 16 rb + c16 (padding
+        // rows take the last row's: their q is zero and their output unused)
+        int qpos[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) qpos[rb] = a.start + min(R0 + 16 * rb + c16, a.rows - 1) / a.g;
         const int last_row_blk = min(a.rows, (b + 1) * kRowsPerBlock) - 1;
         const int kend = a.start + last_row_blk / a.g + 1;
         const int ntiles = (kend + kKeysPerTile - 1) / kKeysPerTile;
@@ -423,7 +439,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         const int pR = R0 + prow;
         const int pqpos = a.start + min(pR, a.rows - 1) / a.g;
         auto pchunk = [&](int i) { return (i / NH4) * (CQ / 2) + pj * NH4 + (i % NH4); };  // fp32 chunk of float4 i
-        half8 qfl[SPLITQ ? QK : 1];  // fp16 residual of q in split-q mode, in the MFMA operand layout
+        half8 qfl[SPLITQ ? 2 : 1][SPLITQ ? KS : 1];  // fp16 residual of q (split-q), B-operand layout [rb][ks]
         {
             // cos/sin float4 q: NeoX the angles of half-0 float4 q (4 * its chunk);
             // block8 / interleaved the four angles 2c .. 2c+3 of chunk pair (c, c+1)
@@ -543,26 +559,31 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
             PQA_PSTAMP(32 * j + kPStQMath, tid == 0);
             if constexpr (SPLITQ) {
                 __syncthreads();  // both waves' residual rows landed
-                const char* lrow = qst + col * HD * 4;
 #pragma unroll
-                for (int ks = 0; ks < QK; ks++)
-                    qfl[ks] = *(const half8*)(lrow + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1))));
+                for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        qfl[rb][ks] = *(const half8*)(qst + (16 * rb + c16) * HD * 4 +
+                                                      16 * ((4 * ks + g16) ^ (c16 & (T::CH - 1))));
             }
         }
-        const char* sq_row = sq[wr] + col * HD * 2;
-        auto qread = [&](int ks) { return *(const half8*)(sq_row + 16 * ((2 * ks + hk) ^ (col & (T::CH - 1)))); };
+        // q fragment of row block rb, k-step ks: row 16 rb + c16, chunk (4 ks + g16) ^ (row mod chunks)
+        const char* sq_lane = sq[wr] + c16 * HD * 2;
+        auto qread = [&](int ks, int rb) {
+            return *(const half8*)(sq_lane + rb * 16 * HD * 2 + 16 * ((4 * ks + g16) ^ (c16 & (T::CH - 1))));
+        };
         PQA_PSTAMP(32 * j + kPStQReady + w, (tid & 63) == 0);
 
         // The running max starts at -1e30 as in the reference (cpp/model.hpp:383):
         // a row whose keys in a tile are all masked (the odd group's first tile
         // can be) then gets p = exp2(-inf) = 0 and a rescale factor of 1, never
         // exp2(-inf - -inf).
-        float m_run = -1e30f, l_run = 0.0f;
-        floatx16 o[DT];
+        float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.0f, 0.0f};  // rows 16 rb + c16
+        floatx4 o[DB][2];  // O^T block (db, rb): dims 16 db + 4 g16 .. +3 of row 16 rb + c16
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+        for (int db = 0; db < DB; db++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+            for (int rb = 0; rb < 2; rb++) o[db][rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
         auto tile = [&](int step, auto BUF) {
             constexpr int buf = decltype(BUF)::value;
@@ -579,94 +600,115 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
 
             const char* kt_lds = lds[buf][par][0];
             const char* vt_lds = lds[buf][par][1];
-            // S^T = K Q^T: k-step ks takes q(ks) and the K fragments of both 32-key
-            // halves; operands come from LDS through a ring RS steps deep, so the
-            // reads run ahead of the MFMAs that consume them.
-            constexpr int RS = 3;
-            floatx16 sacc[2];
-            half8 rq[RS], rk0[RS], rk1[RS];
+            // S^T = K Q^T in 16x16 blocks (key block kb, row block rb), KS
+            // k-steps of 32 dims: 8 independent accumulators. Operands come from
+            // LDS ahead of the MFMAs that use them: q one k-step ahead, K
+            // fragments (sequence f = 4 ks + kb) through a ring RK deep.
+            constexpr int RK = 4;
+            floatx4 sacc[4][2];
+            half8 rq[2][2], rk[RK];
+            auto kread = [&](int f) {
+                return *(const half8*)(kt_lds + (f & 3) * 16 * T::ROWB + koff[f >> 2]);
+            };
+            rq[0][0] = qread(0, 0);
+            rq[0][1] = qread(0, 1);
 #pragma unroll
-            for (int i = 0; i < RS; i++) {
-                rq[i] = qread(i);
-                rk0[i] = *(const half8*)(kt_lds + koff[i]);
-                rk1[i] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[i]);
-            }
+            for (int f = 0; f < RK; f++) rk[f] = kread(f);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ks = 0; ks < QK; ks++) {
-                const int sl = ks % RS;
-                const half8 qv = rq[sl], k0 = rk0[sl], k1 = rk1[sl];
-                if (ks + RS < QK) {
-                    rq[sl] = qread(ks + RS);
-                    rk0[sl] = *(const half8*)(kt_lds + koff[ks + RS]);
-                    rk1[sl] = *(const half8*)(kt_lds + 32 * T::ROWB + koff[ks + RS]);
+            for (int ks = 0; ks < KS; ks++) {
+                if (ks + 1 < KS) {
+                    rq[(ks + 1) & 1][0] = qread(ks + 1, 0);
+                    rq[(ks + 1) & 1][1] = qread(ks + 1, 1);
                 }
-                // keep the reads ahead: the scheduler would otherwise sink them
-                // next to their MFMAs and expose the LDS latency again
-                __builtin_amdgcn_sched_barrier(0);
-                if (ks == 0) {
-                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, floatx16{}, 0, 0, 0);
-                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, floatx16{}, 0, 0, 0);
-                } else {
-                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qv, sacc[0], 0, 0, 0);
-                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qv, sacc[1], 0, 0, 0);
-                }
-                if constexpr (SPLITQ) {
-                    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qfl[ks], sacc[0], 0, 0, 0);
-                    sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qfl[ks], sacc[1], 0, 0, 0);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const int f = 4 * ks + kb;
+                    const half8 kf = rk[f % RK];
+                    if (f + RK < 4 * KS) rk[f % RK] = kread(f + RK);
+                    // keep the reads ahead: the scheduler would otherwise sink them
+                    // next to their MFMAs and expose the LDS latency again
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int rb = 0; rb < 2; rb++)
+                        sacc[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            kf, rq[ks & 1][rb], ks == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : sacc[kb][rb], 0, 0, 0);
+                    if constexpr (SPLITQ) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; rb++)
+                            sacc[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[rb][ks], sacc[kb][rb], 0, 0, 0);
+                    }
                 }
             }
-            // lane holds keys key0 + 32*t2 + 8*(r/4) + 4*hk + r%4 of q row `col`
+            // lane holds keys key0 + 16 kb + 4 g16 + e (e < 4) of rows 16 rb + c16
             if (key0 + kKeysPerTile - 1 > qpos_min_w) {
 #pragma unroll
-                for (int t2 = 0; t2 < 2; t2++)
+                for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int key = key0 + 32 * t2 + 8 * (r >> 2) + 4 * hk + (r & 3);
-                        if (key > qpos) sacc[t2][r] = NEG_INF;
-                    }
+                    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (key0 + 16 * kb + 4 * g16 + e > qpos[rb]) sacc[kb][rb][e] = NEG_INF;
             }
-            float mx = NEG_INF;
+            // row maximum: the lane's 16 scores, then the row's 4 lanes (c16 + 16 g)
+            float mx[2];
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
+            for (int rb = 0; rb < 2; rb++) {
+                float m = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
 #pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[t2][r]);
-            mx = max_x32(mx);
+                for (int kb = 1; kb < 4; kb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) m = fmaxf(m, sacc[kb][rb][e]);
+                mx[rb] = max_x32(max_x16(m));
+            }
             PQA_SSTAMP(step, kSStScores);
-            if (__any(mx > m_run + kRescaleSlack)) {
-                const float m_new = fmaxf(m_run, mx);
-                const float corr = fast_exp2(m_run - m_new);
-                m_run = m_new;
-                l_run *= corr;
+            if (__any(mx[0] > m_run[0] + kRescaleSlack || mx[1] > m_run[1] + kRescaleSlack)) {
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++)
+                for (int rb = 0; rb < 2; rb++) {
+                    const float m_new = fmaxf(m_run[rb], mx[rb]);
+                    const float corr = fast_exp2(m_run[rb] - m_new);
+                    m_run[rb] = m_new;
+                    l_run[rb] *= corr;
 #pragma unroll
-                    for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+                    for (int db = 0; db < DB; db++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) o[db][rb][e] *= corr;
+                }
             }
-            half8 pf[4];
+            // P^T as the B operand of the PV product, 32 keys per k-step s: k
+            // elements 8 g16 .. +3 are keys 32 s + 4 g16 .. +3 (key block 2 s),
+            // 8 g16 + 4 .. +7 are keys 32 s + 16 + 4 g16 .. +3 (block 2 s + 1),
+            // exactly the lane's own scores, so P never leaves registers.
+            half8 pf[2][2];  // [rb][s]
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
+            for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) pf[2 * t2 + (r >> 3)][r & 7] = (_Float16)fast_exp2(sacc[t2][r] - m_run);
-            // row sum of the fp16 P the PV product consumes (v_dot2_f32_f16 with ones)
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        pf[rb][kb >> 1][4 * (kb & 1) + e] = (_Float16)fast_exp2(sacc[kb][rb][e] - m_run[rb]);
+            // row sums of the fp16 P the PV product consumes (v_dot2_f32_f16 with ones)
             const half2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-            float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < 4; s++)
+            for (int rb = 0; rb < 2; rb++) {
+                float ps[2] = {0.0f, 0.0f};
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    ps[s] = __builtin_amdgcn_fdot2(half2{pf[s][2 * e], pf[s][2 * e + 1]}, one2, ps[s], false);
-            l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+                for (int s = 0; s < 2; s++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        ps[s] = __builtin_amdgcn_fdot2(half2{pf[rb][s][2 * e], pf[rb][s][2 * e + 1]}, one2, ps[s], false);
+                l_run[rb] += ps[0] + ps[1];
+            }
             PQA_SSTAMP(step, kSStSoftmax);
-            // O^T += V^T P^T: 4 key steps x DT dim tiles; V^T fragments (two
-            // transposing reads each) through a ring RV MFMAs deep.
-            constexpr int NPV = 4 * DT, RV = 4;
+            // O^T += V^T P^T: 2 key steps x DB dim blocks x 2 row blocks; V^T
+            // fragments (two transposing reads each) through a ring RV deep.
+            constexpr int NPV = 2 * DB, RV = 4;
             auto vread = [&](int idx) {
-                const int s = idx / DT, dt = idx % DT;
+                const int s = idx / DB, db = idx % DB;
                 half4 part[2];
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    const char* adr = vt_lds + voff[dt] + (16 * s + 8 * t) * T::ROWB;
+                    const char* adr = vt_lds + voff[db] + (32 * s + 16 * t) * T::ROWB;
                     const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)adr);
                     part[t] = __builtin_bit_cast(half4, raw);
                 }
@@ -681,7 +723,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
                 const half8 vf = rv[idx % RV];
                 if (idx + RV < NPV) rv[idx % RV] = vread(idx + RV);
                 __builtin_amdgcn_sched_barrier(0);
-                o[idx % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[idx / DT], o[idx % DT], 0, 0, 0);
+                const int s = idx / DB, db = idx % DB;
+#pragma unroll
+                for (int rb = 0; rb < 2; rb++)
+                    o[db][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[rb][s], o[db][rb], 0, 0, 0);
             }
             PQA_SSTAMP(step, kSStPV);
         };
@@ -694,54 +739,61 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
 
         PQA_PSTAMP(32 * j + kPStLoop + w, (tid & 63) == 0);
         // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
-        // LDS: [wr][MR][64 lanes] floats: o (16 DT per lane), m, l.
-        constexpr int MR = 16 * DT + 2;
+        // LDS: [wr][MR][64 lanes] floats: o (DB x 2 x 4 per lane), m (2), l (2).
+        constexpr int MR = 8 * DB + 4;
         static_assert(kGroupWaves * MR * 64 * 4 <= (int)sizeof(lds), "merge area exceeds the tile buffers");
         __syncthreads();  // tile buffers are free
         float* mg = (float*)&lds[0][0][0][0] + wr * MR * 64;
         if (par == 1) {
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+            for (int db = 0; db < DB; db++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) mg[(16 * dt + r) * 64 + lane] = o[dt][r];
-            mg[(MR - 2) * 64 + lane] = m_run;
-            mg[(MR - 1) * 64 + lane] = l_run;
+                for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) mg[((db * 2 + rb) * 4 + e) * 64 + lane] = o[db][rb][e];
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) {
+                mg[(MR - 4 + rb) * 64 + lane] = m_run[rb];
+                mg[(MR - 2 + rb) * 64 + lane] = l_run[rb];
+            }
         }
         __syncthreads();
         PQA_PSTAMP(32 * j + kPStMerged, tid == 0);
         if (par == 0) {
-            {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) {
                 // the row's 1/l folded into both weights: one multiply and one
                 // fused multiply-add per output value (the output is not stored
-                // in any reference rounding order, only within the tolerance)
-                const float mo = mg[(MR - 2) * 64 + lane], lo = mg[(MR - 1) * 64 + lane];
-                const float M = fmaxf(m_run, mo);
-                const float fe = fast_exp2(m_run - M);
+                // in any reference rounding order, only within the tolerance);
+                // l sums the row's 4 lanes
+                const float mo = mg[(MR - 4 + rb) * 64 + lane], lo = mg[(MR - 2 + rb) * 64 + lane];
+                const float M = fmaxf(m_run[rb], mo);
+                const float fe = fast_exp2(m_run[rb] - M);
                 const float fo = fast_exp2(mo - M);
-                const float inv = 1.0f / sum_x32(fmaf(l_run, fe, lo * fo));
+                const float inv = 1.0f / sum_x32(sum_x16(fmaf(l_run[rb], fe, lo * fo)));
                 const float we = fe * inv, wo = fo * inv;
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++)
+                for (int db = 0; db < DB; db++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) o[dt][r] = fmaf(o[dt][r], we, mg[(16 * dt + r) * 64 + lane] * wo);
+                    for (int e = 0; e < 4; e++)
+                        o[db][rb][e] = fmaf(o[db][rb][e], we, mg[((db * 2 + rb) * 4 + e) * 64 + lane] * wo);
             }
 
             // ---- normalise and store ----
             // The wave's 32 rows go through its own merge area (read above; LDS
             // operations of one wave run in order) as [row][HD] fp32, 16-byte chunk c
             // of row r at slot c ^ (r mod chunks), so that each store instruction
-            // writes whole 512-byte output rows instead of 32-byte pieces of 32 rows.
+            // writes whole 512-byte output rows instead of pieces of 32 rows.
             constexpr int CPR = HD / 4;  // 16-byte chunks per output row
             static_assert(32 * HD <= MR * 64, "output staging exceeds the merge area");
             const int orow = rvalid ? tok * a.nh + hq : -1;  // output row of q row `col`
             wave_sync();
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+            for (int db = 0; db < DB; db++)
 #pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    const int c = 8 * dt + 2 * r4 + hk;  // dims 32 dt + 8 r4 + 4 hk .. +3
-                    *(floatx4*)(mg + col * HD + 4 * (c ^ (col & (CPR - 1)))) =
-                        floatx4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
+                for (int rb = 0; rb < 2; rb++) {
+                    const int r = 16 * rb + c16, c = 4 * db + g16;  // dims 16 db + 4 g16 .. +3
+                    *(floatx4*)(mg + r * HD + 4 * (c ^ (r & (CPR - 1)))) = o[db][rb];
                 }
             wave_sync();
 #pragma unroll
