@@ -39,6 +39,7 @@ import os
 import subprocess
 import sys
 import time
+import warnings
 
 import numpy as np
 
@@ -1114,7 +1115,9 @@ def prefill_phase_stamps(reps=5):
         ends = np.nanmax(np.where(a > 0, a, np.nan), 1)
         rows.append((len(a), rel, (np.nanmax(ends) - a[:, 0].min()) / 100.0,
                      (a[:, 0].max() - a[:, 0].min()) / 100.0))
-    med = np.nanmedian(np.stack([np.nanmean(r, 0) for _, r, _, _ in rows]), 0)
+    with warnings.catch_warnings():  # stamp slots no wave writes are all-NaN columns
+        warnings.simplefilter("ignore", RuntimeWarning)
+        med = np.nanmedian(np.stack([np.nanmean(r, 0) for _, r, _, _ in rows]), 0)
     span = float(np.median([x[2] for x in rows]))
     spread = float(np.median([x[3] for x in rows]))
     lines = [f"prefill 2048 tokens, 32/8 heads, hd 128, QK-norm, hi + lo q: {rows[0][0]} workgroups; "
