@@ -763,82 +763,105 @@ __global__ __launch_bounds__(kAttnThreads, 1) void prefill_attn_kernel(const Att
         }
 
         PQA_PSTAMP(32 * j + kPStLoop + w, (tid & 63) == 0);
-        // ---- merge the odd-tile partial (wave w + 4) into the even one (wave w) ----
-        // LDS: [wr][MR][64 lanes] floats: o (DB x 2 x 4 per lane), m (2), l (2).
-        constexpr int MR = 8 * DB + 4;
-        static_assert(kGroupWaves * MR * 64 * 4 <= (int)sizeof(lds), "merge area exceeds the tile buffers");
+        // ---- merge the two parities' partials; each wave finishes one row block ----
+        // The even-tile wave finishes rows 0..15 of the row group (row block 0)
+        // and the odd-tile wave rows 16..31, so merging and storing are split
+        // between the two waves of a SIMD (one wave storing all 32 rows took
+        // 3 us more per Qwen3-4B layer: the stores are issue-bound per wave).
+        // Each wave hands the other the half of its partial the other
+        // finishes: LDS X[par][wr] holds, per lane, the DB float4s of O of
+        // that row block and one float4 (m, l, 0, 0), as [slot][lane][4]
+        // (16-byte accesses, conflict-free).
+        constexpr int XS = DB + 1;  // float4 slots per lane
+        constexpr int XB = XS * 64 * 16;  // bytes per wave
+        constexpr int CPR = HD / 4;       // 16-byte chunks per output row
+        constexpr int SB = 16 * HD * 4;   // staging bytes per wave: 16 rows of HD fp32
+        static_assert(2 * kGroupWaves * XB + kGroupWaves * SB <= (int)sizeof(lds), "merge areas exceed the tile buffers");
+        static_assert(SB <= (int)sizeof(sq[0]), "even-tile staging exceeds the q area");
         __syncthreads();  // tile buffers are free
-        float* mg = (float*)&lds[0][0][0][0] + wr * MR * 64;
-        if (par == 1) {
+        // RBO: the row block this wave finishes (a constant in each branch, so
+        // o, m and l stay in registers)
+        auto hand_over = [&](auto RBO) {
+            constexpr int rbo = decltype(RBO)::value;
+            floatx4* mine = (floatx4*)&lds[0][0][0][0] + (size_t)(par * kGroupWaves + wr) * XS * 64;
+#pragma unroll
+            for (int db = 0; db < DB; db++) mine[db * 64 + lane] = o[db][rbo ^ 1];
+            mine[DB * 64 + lane] = floatx4{m_run[rbo ^ 1], l_run[rbo ^ 1], 0.0f, 0.0f};
+        };
+        auto finish = [&](auto RBO) {
+            constexpr int rbo = decltype(RBO)::value;
+            const floatx4* other = (const floatx4*)&lds[0][0][0][0] + (size_t)((par ^ 1) * kGroupWaves + wr) * XS * 64;
+            floatx4 po[DB];
+#pragma unroll
+            for (int db = 0; db < DB; db++) po[db] = other[db * 64 + lane];
+            const floatx4 ml = other[DB * 64 + lane];
+            // the even-tile partial (e) and the odd-tile one (o) in the same
+            // roles whichever wave merges, so both row blocks round alike: the
+            // row's 1/l folded into both weights, one multiply and one fused
+            // multiply-add per output value; l sums the row's 4 lanes
+            const float me = rbo == 0 ? m_run[rbo] : ml[0], le = rbo == 0 ? l_run[rbo] : ml[1];
+            const float mo = rbo == 0 ? ml[0] : m_run[rbo], lo = rbo == 0 ? ml[1] : l_run[rbo];
+            const float M = fmaxf(me, mo);
+            const float fe = fast_exp2(me - M);
+            const float fo = fast_exp2(mo - M);
+            const float inv = 1.0f / sum_x32(sum_x16(fmaf(le, fe, lo * fo)));
+            const float we = fe * inv, wo = fo * inv;
 #pragma unroll
             for (int db = 0; db < DB; db++)
 #pragma unroll
-                for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) mg[((db * 2 + rb) * 4 + e) * 64 + lane] = o[db][rb][e];
-#pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
-                mg[(MR - 4 + rb) * 64 + lane] = m_run[rb];
-                mg[(MR - 2 + rb) * 64 + lane] = l_run[rb];
-            }
-        }
-        __syncthreads();
-        PQA_PSTAMP(32 * j + kPStMerged, tid == 0);
-        if (par == 0) {
-#pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
-                // the row's 1/l folded into both weights: one multiply and one
-                // fused multiply-add per output value (the output is not stored
-                // in any reference rounding order, only within the tolerance);
-                // l sums the row's 4 lanes
-                const float mo = mg[(MR - 4 + rb) * 64 + lane], lo = mg[(MR - 2 + rb) * 64 + lane];
-                const float M = fmaxf(m_run[rb], mo);
-                const float fe = fast_exp2(m_run[rb] - M);
-                const float fo = fast_exp2(mo - M);
-                const float inv = 1.0f / sum_x32(sum_x16(fmaf(l_run[rb], fe, lo * fo)));
-                const float we = fe * inv, wo = fo * inv;
-#pragma unroll
-                for (int db = 0; db < DB; db++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        o[db][rb][e] = fmaf(o[db][rb][e], we, mg[((db * 2 + rb) * 4 + e) * 64 + lane] * wo);
-            }
+                for (int e = 0; e < 4; e++) {
+                    const float xe = rbo == 0 ? o[db][rbo][e] : po[db][e];
+                    const float xo = rbo == 0 ? po[db][e] : o[db][rbo][e];
+                    o[db][rbo][e] = fmaf(xe, we, xo * wo);
+                }
 
             // ---- normalise and store ----
-            // The wave's 32 rows go through its own merge area (read above; LDS
-            // operations of one wave run in order) as [row][HD] fp32, 16-byte chunk c
-            // of row r at slot c ^ (r mod chunks), so that each store instruction
-            // writes whole 512-byte output rows instead of pieces of 32 rows.
-            constexpr int CPR = HD / 4;  // 16-byte chunks per output row
-            static_assert(32 * HD <= MR * 64, "output staging exceeds the merge area");
-            const int orow = rvalid ? tok * a.nh + hq : -1;  // output row of q row `col`
+            // The wave's 16 rows go through LDS (the even-tile waves' own q
+            // area, the odd-tile waves' a slot past the exchange areas) as
+            // [row][HD] fp32, 16-byte chunk c of row r at slot c ^ (r mod
+            // chunks), so that each store instruction writes whole 512-byte
+            // output rows.
+            float* stg = par == 0 ? (float*)&sq[wr][0]
+                                  : (float*)((char*)&lds[0][0][0][0] + 2 * kGroupWaves * XB + wr * SB);
+#pragma unroll
+            for (int db = 0; db < DB; db++) {
+                const int c = 4 * db + g16;  // dims 16 db + 4 g16 .. +3
+                *(floatx4*)(stg + c16 * HD + 4 * (c ^ (c16 & (CPR - 1)))) = o[db][rbo];
+            }
+            // output row of q row 16 rbo + (lane & 15)
+            const int Rl = R0 + 16 * rbo + c16;
+            const int orow = Rl < a.rows ? (Rl / a.g) * a.nh + kvh * a.g + (Rl - (Rl / a.g) * a.g) : -1;
             wave_sync();
+            constexpr int RPS = 64 / CPR;          // rows per store instruction
+            constexpr int NST = 16 * CPR / 64;     // store instructions per wave
+            floatx4 vv[NST];
 #pragma unroll
-            for (int db = 0; db < DB; db++)
-#pragma unroll
-                for (int rb = 0; rb < 2; rb++) {
-                    const int r = 16 * rb + c16, c = 4 * db + g16;  // dims 16 db + 4 g16 .. +3
-                    *(floatx4*)(mg + r * HD + 4 * (c ^ (r & (CPR - 1)))) = o[db][rb];
-                }
-            wave_sync();
-#pragma unroll
-            for (int i = 0; i < 32 * CPR / 64; i++) {
-                constexpr int RPS = 64 / CPR;  // rows per store instruction
+            for (int i = 0; i < NST; i++) {
                 const int rr = RPS * i + lane / CPR, c = lane % CPR;
+                vv[i] = *(const floatx4*)(stg + rr * HD + 4 * (c ^ (rr & (CPR - 1))));
+            }
+#pragma unroll
+            for (int i = 0; i < NST; i++) {
+                const int c = lane % CPR;
                 int orr = -1;
 #pragma unroll
                 for (int u = 0; u < RPS; u++) {
                     const int v = __builtin_amdgcn_readlane(orow, RPS * i + u);
                     if (lane / CPR == u) orr = v;
                 }
-                const floatx4 vv = *(const floatx4*)(mg + rr * HD + 4 * (c ^ (rr & (CPR - 1))));
                 if (orr >= 0) {
-                    if constexpr (kNtOut) __builtin_nontemporal_store(vv, (floatx4*)(a.out + (size_t)orr * HD + 4 * c));
-                    else *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv;
+                    if constexpr (kNtOut) __builtin_nontemporal_store(vv[i], (floatx4*)(a.out + (size_t)orr * HD + 4 * c));
+                    else *(floatx4*)(a.out + (size_t)orr * HD + 4 * c) = vv[i];
                 }
             }
-            PQA_PSTAMP(32 * j + kPStStored + w, lane == 0);
-        }
+        };
+        if (par == 0) hand_over(std::integral_constant<int, 0>{});
+        else hand_over(std::integral_constant<int, 1>{});
+        __syncthreads();
+        PQA_PSTAMP(32 * j + kPStMerged, tid == 0);
+        if (par == 0) finish(std::integral_constant<int, 0>{});
+        else finish(std::integral_constant<int, 1>{});
+        PQA_PSTAMP(32 * j + kPStStored + wr, lane == 0 && par == 0);
     }
 }
 
